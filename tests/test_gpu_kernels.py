@@ -1,0 +1,106 @@
+"""GPU parity for the integer/index parts: generator, weight pack, routing and
+dispatch -- all bit-exact against the oracle and the golden fixtures."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import pack as opack
+from oracle import routing
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_generator_matches_host(ops, cuda):
+    for seed, stream, n in [(1, 5, 1 << 20), (0x15642001, 7, 3 * 7168 + 5)]:
+        t = torch.empty(n, dtype=torch.uint8, device=cuda)
+        ops.fill_normal_e4m3_(t, seed, stream)
+        assert np.array_equal(t.cpu().numpy(), ops.host_normal_e4m3(n, seed, stream))
+
+
+def test_pack_matches_oracle_permutation(ops, cuda):
+    g = torch.Generator(device="cpu").manual_seed(5)
+    w13 = torch.randint(0, 256, (2, 4096, 7168), dtype=torch.uint8, generator=g)
+    w2 = torch.randint(0, 256, (2, 7168, 2048), dtype=torch.uint8, generator=g)
+    p13 = ops.pack_w13(w13.to(cuda))
+    p2 = ops.pack_w2(w2.to(cuda))
+    assert np.array_equal(p13.cpu().view(torch.uint8).numpy().reshape(-1), opack.pack_w13(w13.numpy()).reshape(-1))
+    assert np.array_equal(p2.cpu().view(torch.uint8).numpy().reshape(-1), opack.pack_w2(w2.numpy()).reshape(-1))
+    assert torch.equal(ops.unpack_w13(p13).cpu(), w13)
+    assert torch.equal(ops.unpack_w2(p2).cpu(), w2)
+
+
+def test_pack_roundtrip_full_size(ops, inputs_mod, cuda):
+    inp = inputs_mod.make_config_inputs(1, device=cuda)
+    w13 = inp["gemm1_weights"].view(torch.uint8)
+    w2 = inp["gemm2_weights"].view(torch.uint8)
+    p13, p2 = ops.pack_w13(inp["gemm1_weights"]), ops.pack_w2(inp["gemm2_weights"])
+    assert p13.numel() * 4 == w13.numel() and p2.numel() * 4 == w2.numel()
+    assert torch.equal(ops.unpack_w13(p13), w13)
+    assert torch.equal(ops.unpack_w2(p2), w2)
+    # spot-check the layout formula on the packed bytes
+    pb = p13.view(torch.uint8).view(32, 16, 56, 16, 2, 64, 16)
+    rng = np.random.default_rng(0)
+    for _ in range(64):
+        e, nb, kb, t, h, lane, b = (int(rng.integers(0, m)) for m in (32, 16, 56, 16, 2, 64, 16))
+        row = (t & 1) * 2048 + nb * 128 + 16 * (t >> 1) + (lane & 15)
+        col = kb * 128 + 32 * (lane >> 4) + 16 * h + b
+        assert int(pb[e, nb, kb, t, h, lane, b]) == int(w13[e, row, col])
+
+
+def _gpu_route(ops, logits, bias, rsf, offset, e_local, cuda):
+    return ops.route(logits.to(cuda).contiguous(), bias.to(torch.float32).reshape(-1).to(cuda).contiguous(),
+                     rsf, offset, e_local)
+
+
+@pytest.mark.parametrize("idx", [0, 1, 2, 3, 4])
+def test_routing_bit_exact(ops, inputs_mod, cuda, idx):
+    cfg = inputs_mod.CONFIGS[idx]
+    small = inputs_mod.host_tensors(cfg)
+    logits, bias = small["routing_logits"], small["routing_bias"]
+    print(f"[route] config {idx} T={cfg.T}", flush=True)
+    got = _gpu_route(ops, logits, bias, cfg.rsf, cfg.local_expert_offset, 32, cuda)
+    ids = got["topk_ids"].cpu().numpy()
+    w = got["topk_w"].cpu().numpy()
+    fx = np.load(GOLDEN / f"routing_cfg{idx}.npz")
+    assert np.array_equal(ids, fx["ids"]), "top-8 sets differ from the reference's routing"
+    ref = routing.route(logits.numpy(), bias.to(torch.float32).numpy(), cfg.rsf)
+    assert np.array_equal(ids, ref["ids"])
+    assert np.array_equal(w.view(np.uint32), ref["weights"].view(np.uint32)), "weights not bit-exact vs oracle"
+    d = routing.local_dispatch(ref["ids"], ref["weights"], cfg.local_expert_offset, 32)
+    assert np.array_equal(got["counts"].cpu().numpy(), d["counts"])
+    assert np.array_equal(got["offsets"].cpu().numpy(), d["offsets"])
+    R = int(d["offsets"][-1])
+    assert np.array_equal(got["route_token"].cpu().numpy()[:R], d["route_token"])
+    assert np.array_equal(got["route_weight"].cpu().numpy()[:R].view(np.uint32), d["route_weight"].view(np.uint32))
+    assert np.array_equal(got["token_route"].cpu().numpy(), d["token_route"])
+
+
+@pytest.mark.parametrize("T,offset,e_local,seed", [(1, 0, 32, 1), (3, 0, 32, 2), (5, -8, 32, 3), (77, 250, 32, 4),
+                                                    (130, 40, 8, 5), (2049, 224, 32, 6), (64, 300, 32, 7)])
+def test_routing_edge_cases(ops, cuda, T, offset, e_local, seed):
+    rng = np.random.default_rng(seed)
+    logits = torch.from_numpy((rng.standard_normal((T, 256)) * 2).astype(np.float32))
+    bias = torch.from_numpy((rng.standard_normal(256) * 0.1).astype(np.float32))
+    got = _gpu_route(ops, logits, bias, 1.7, offset, e_local, cuda)
+    ref = routing.route(logits.numpy(), bias.numpy(), 1.7)
+    assert np.array_equal(got["topk_ids"].cpu().numpy(), ref["ids"])
+    assert np.array_equal(got["topk_w"].cpu().numpy().view(np.uint32), ref["weights"].view(np.uint32))
+    d = routing.local_dispatch(ref["ids"], ref["weights"], offset, e_local)
+    R = int(d["offsets"][-1])
+    assert np.array_equal(got["offsets"].cpu().numpy(), d["offsets"])
+    assert np.array_equal(got["route_token"].cpu().numpy()[:R], d["route_token"])
+    assert np.array_equal(got["token_route"].cpu().numpy(), d["token_route"])
+
+
+def test_routing_exact_ties(ops, cuda):
+    logits = torch.zeros((4, 256), dtype=torch.float32)
+    logits[1, 100:140] = 1.0  # equal values straddling two groups
+    bias = torch.zeros(256)
+    got = _gpu_route(ops, logits, bias, 1.0, 0, 32, cuda)
+    ref = routing.route(logits.numpy(), bias.numpy(), 1.0)
+    assert np.array_equal(got["topk_ids"].cpu().numpy(), ref["ids"])
+    assert got["topk_ids"][0].tolist() == list(range(8))
