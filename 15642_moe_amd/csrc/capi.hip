@@ -258,6 +258,17 @@ int moe_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id,
                     "fill_normal_e4m3_kernel launch");
 }
 
+int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream) {
+  if (n < 0) return fail(MOE_ERR_INVALID_ARG, "n must be >= 0, got %d", n);
+  if (n == 0) return MOE_OK;
+  MOE_TRY(check_ptr(a, "a"));
+  MOE_TRY(check_ptr(b, "b"));
+  MOE_TRY(check_ptr(d, "d"));
+  return hip_status(moe::launch_mfma_tiles(static_cast<const uint8_t*>(a), static_cast<const uint8_t*>(b), d, n,
+                                           reinterpret_cast<hipStream_t>(stream)),
+                    "mfma_tile_kernel launch");
+}
+
 int moe_host_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id, uint64_t first_index,
                               int threads) {
   if (n == 0) return MOE_OK;

@@ -384,6 +384,29 @@ stage2_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, cons
   }
 }
 
+// n independent D = A x B products of 16x128 by 128x16 e4m3 tiles (A row-major,
+// B given as its 16 columns, K contiguous), through the same MFMA wrapper the
+// GEMMs use: lets tests measure the instruction's accumulation accuracy.
+__global__ void __launch_bounds__(64)
+mfma_tile_kernel(const uint8_t* __restrict__ A, const uint8_t* __restrict__ B, float* __restrict__ D, int n) {
+  const int t = blockIdx.x, l = threadIdx.x;
+  if (t >= n) return;
+  const uint8_t* pa = A + (size_t)t * TILE_BYTES + (l & 15) * 128 + (l >> 4) * 32;
+  const uint8_t* pb = B + (size_t)t * TILE_BYTES + (l & 15) * 128 + (l >> 4) * 32;
+  const v8i a = make_v8i(*reinterpret_cast<const uint4*>(pa), *reinterpret_cast<const uint4*>(pa + 16));
+  const v8i b = make_v8i(*reinterpret_cast<const uint4*>(pb), *reinterpret_cast<const uint4*>(pb + 16));
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  const v4f d = mfma_16x16x128_fp8(a, b, zero4);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) D[(size_t)t * 256 + (4 * (l >> 4) + v) * 16 + (l & 15)] = d[v];
+}
+
+hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  mfma_tile_kernel<<<n, 64, 0, stream>>>(A, B, D, n);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------

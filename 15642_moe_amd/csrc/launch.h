@@ -29,4 +29,6 @@ hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
                          float* Y, int T, int e_local, int max_routes, hipStream_t stream);
 
+hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n, hipStream_t stream);
+
 }  // namespace moe

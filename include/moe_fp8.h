@@ -136,6 +136,15 @@ int moe_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id,
 int moe_host_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id, uint64_t first_index,
                               int threads);
 
+/*
+ * n independent 16x16 products D[t] = A[t] (16x128 e4m3, row-major) x B[t]
+ * (128x16 e4m3, given as 16 columns of 128 contiguous K bytes) through the
+ * FP8 MFMA instruction the GEMMs use; D fp32 [n, 16, 16] row-major.  Test
+ * instrumentation for the instruction's accumulation accuracy; no
+ * counterpart in the reference.
+ */
+int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

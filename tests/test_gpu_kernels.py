@@ -21,6 +21,39 @@ def test_device_generator_matches_host(ops, cuda):
         assert np.array_equal(t.cpu().numpy(), ops.host_normal_e4m3(n, seed, stream))
 
 
+# Measured bound on the FP8 MFMA's block-sum error, relative to sum |a*b|
+# over the 128 products (the instruction does not round the exact sum to
+# fp32; see test_mfma_block_sum_accuracy).  The parity gates use it.
+MFMA_REL_BOUND = 2.5e-4
+
+
+@pytest.mark.parametrize("dist", ["full_range", "normal"])
+def test_mfma_block_sum_accuracy(capi, lib, cuda, dist):
+    import ctypes
+
+    from oracle.numerics import E4M3_TABLE, e4m3_encode
+
+    n = 4096
+    rng = np.random.default_rng(11)
+    if dist == "full_range":
+        codes = rng.integers(0, 256, size=(2, n, 16, 128), dtype=np.uint8)
+        codes[(codes & 0x7F) == 0x7F] = 0  # no NaN encodings
+    else:
+        codes = e4m3_encode(rng.standard_normal((2, n, 16, 128)).astype(np.float32))
+    a, b = torch.from_numpy(codes[0]).to(cuda), torch.from_numpy(codes[1]).to(cuda)
+    d = torch.empty((n, 16, 16), dtype=torch.float32, device=cuda)
+    capi.check(lib.moe_mfma_tiles(ctypes.c_void_p(a.data_ptr()), ctypes.c_void_p(b.data_ptr()),
+                                  ctypes.c_void_p(d.data_ptr()), n, None), "moe_mfma_tiles")
+    got = d.cpu().numpy().astype(np.float64)
+    A, B = torch.from_numpy(E4M3_TABLE[codes[0]]), torch.from_numpy(E4M3_TABLE[codes[1]])
+    exact = torch.bmm(A, B.transpose(1, 2)).numpy()
+    mag = torch.bmm(A.abs(), B.abs().transpose(1, 2)).numpy()
+    rel = np.abs(got - exact) / np.maximum(mag, 1e-30)
+    rn = np.mean(got == exact.astype(np.float32))
+    print(f"[mfma] {dist}: worst |err|/sum|ab| = {rel.max():.3e}, equal to RN32(exact): {rn:.4f}", flush=True)
+    assert rel.max() <= MFMA_REL_BOUND
+
+
 def test_pack_matches_oracle_permutation(ops, cuda):
     g = torch.Generator(device="cpu").manual_seed(5)
     w13 = torch.randint(0, 256, (2, 4096, 7168), dtype=torch.uint8, generator=g)
