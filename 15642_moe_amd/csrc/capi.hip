@@ -212,18 +212,33 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
   MOE_TRY(hip_status(moe::launch_route(logits, bias, routed_scaling_factor, T, topk_ids, topk_w, st),
                      "route_kernel launch"));
   MOE_TRY(mark(1));
-  MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,
-                                          route_token, route_weight, token_route, st),
-                     "dispatch_kernel launch"));
-  MOE_TRY(mark(2));
-  MOE_TRY(hip_status(moe::launch_stage1(static_cast<const uint8_t*>(hidden), hidden_scale,
-                                        static_cast<const uint8_t*>(w13_packed), w13_scale, counts, offsets,
-                                        route_token, Cq, Cs, T, e_local, R, st),
-                     "stage1_kernel launch"));
-  MOE_TRY(mark(3));
-  MOE_TRY(hip_status(moe::launch_stage2(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts, offsets,
-                                        route_weight, Y, T, e_local, R, st),
-                     "stage2_kernel launch"));
+  if (T <= moe::DECODE_MAX_T) {
+    // decode path: the local dispatch runs inside GEMM1; its fp32 SwiGLU
+    // output borrows the Y buffer until the FP8 requant has consumed it
+    MOE_TRY(mark(2));
+    MOE_TRY(hip_status(moe::launch_stage1_decode(topk_ids, topk_w, T, e_local, local_expert_offset,
+                                                 static_cast<const uint8_t*>(hidden), hidden_scale,
+                                                 static_cast<const uint8_t*>(w13_packed), w13_scale, counts, offsets,
+                                                 route_token, route_weight, token_route, /*Cf=*/Y, Cq, Cs, st),
+                       "stage1_decode_kernel launch"));
+    MOE_TRY(mark(3));
+    MOE_TRY(hip_status(moe::launch_stage2_decode(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts,
+                                                 offsets, route_weight, Y, e_local, st),
+                       "stage2_decode_kernel launch"));
+  } else {
+    MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,
+                                            route_token, route_weight, token_route, st),
+                       "dispatch_kernel launch"));
+    MOE_TRY(mark(2));
+    MOE_TRY(hip_status(moe::launch_stage1(static_cast<const uint8_t*>(hidden), hidden_scale,
+                                          static_cast<const uint8_t*>(w13_packed), w13_scale, counts, offsets,
+                                          route_token, Cq, Cs, T, e_local, R, st),
+                       "stage1_kernel launch"));
+    MOE_TRY(mark(3));
+    MOE_TRY(hip_status(moe::launch_stage2(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts, offsets,
+                                          route_weight, Y, T, e_local, R, st),
+                       "stage2_kernel launch"));
+  }
   MOE_TRY(mark(4));
   MOE_TRY(hip_status(moe::launch_combine(Y, token_route, T, static_cast<uint16_t*>(out_bf16), st),
                      "combine_kernel launch"));

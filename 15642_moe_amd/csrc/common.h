@@ -23,6 +23,8 @@ constexpr int IB = I / BLK;        // 16 intermediate blocks
 constexpr int G1B = G1 / BLK;      // 32 W13 row blocks
 constexpr int MAX_E_LOCAL = 32;    // dispatch uses a 32-bit local-expert mask per token
 constexpr float E4M3_MAX = 448.0f;
+// Largest token count served by the decode kernels (dispatch fused into GEMM1).
+constexpr int DECODE_MAX_T = 128;
 
 // One MFMA operand tile: 16 rows x 128 K-bytes = 2 KB.  Lane l holds row
 // (l % 16) and K-bytes [32*(l/16), 32*(l/16)+32) as 8 dwords.  This is the
@@ -83,6 +85,18 @@ __host__ __device__ __forceinline__ uint16_t bf16_rne(float x) {
 // v_cvt_pk_fp8_f32: RNE, non-saturating; callers clamp to +-448 first.
 __device__ __forceinline__ uint32_t cvt2_e4m3(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+}
+
+// Bit le is set when the token (its 8 picks in ids) picked global expert
+// le + offset; 1 <= e_local <= 32.
+__device__ __forceinline__ uint32_t local_mask(const int32_t* ids, int offset, int e_local) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k) {
+    const int le = ids[k] - offset;
+    if (le >= 0 && le < e_local) m |= 1u << le;
+  }
+  return m;
 }
 
 // Counter-based generator (splitmix64 finaliser), shared bit-for-bit with

@@ -199,6 +199,7 @@ stage1_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__ hsca
     st.store(s_act[0], s_asc[0], tid);
     __syncthreads();
 
+#pragma unroll 1
     for (int kb0 = 0; kb0 < HB; kb0 += NR) {
 #pragma unroll
       for (int s = 0; s < NR; ++s) {
@@ -336,6 +337,7 @@ stage2_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, cons
     st.store(s_act[0], s_asc[0], tid);
     __syncthreads();
 
+#pragma unroll 1
     for (int kb0 = 0; kb0 < IB; kb0 += NR) {
 #pragma unroll
       for (int s = 0; s < NR; ++s) {
@@ -381,6 +383,244 @@ stage2_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, cons
       }
     }
     __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Decode variants (small T).  Streaming the weights of the hit experts is the
+// whole cost, and a CU streams at a bounded rate (~35-40 GB/s), so the work is
+// cut into thousands of single-wave items (one per (expert, weight slice))
+// that spread evenly over the 256 CUs.  Each wave loads its weight tiles and
+// the 16-route activation fragment straight into registers through an
+// NR-deep ring: no LDS and no barrier in the K loop.  A static grid covers
+// every (expert, slice) pair in expert-major order; since workgroup p runs on
+// XCD p % 8, every expert's slices are dealt round-robin over all XCDs, so the
+// load stays even whichever experts the routing hits.  Experts without routes
+// exit at once.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice) {
+  e = p / nslice;
+  slice = p - e * nslice;
+}
+
+// Stage 1, one wave per (expert e, gate/up tile pair j): 16 I columns,
+// c = gate * silu(up) written in fp32 to Cf [R, 2048] (the FP8 requant needs
+// the amax over 128 columns, i.e. 8 items, and runs in quant_kernel).  The
+// local dispatch is fused into the prologue: every item ranks the T x 8 picks
+// with wave ballots (counts, offsets, its expert's tokens in token order);
+// items j == 0 publish their expert's route arrays, item (0, 0) the counts,
+// offsets and the -1 tails of token_route.
+template <int NR>
+__global__ void __launch_bounds__(64)
+stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
+                     int offset, const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
+                     const uint8_t* __restrict__ w13p, const float* __restrict__ w13s, int32_t* __restrict__ counts,
+                     int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
+                     float* __restrict__ route_weight, int32_t* __restrict__ token_route, float* __restrict__ Cf) {
+  constexpr int BM = 16, NPAIR = I / 16;
+  static_assert(HB % NR == 0, "ring depth must divide the K-block count");
+  __shared__ int s_tok[DECODE_MAX_T];
+  const int lane = threadIdx.x;
+  int e, j;
+  decode_map(blockIdx.x, NPAIR, e, j);
+  if (e >= e_local) return;
+
+  // ---- dispatch: masks of the tokens this lane reads (T <= 128 -> 2 per lane)
+  constexpr int TPL = DECODE_MAX_T / 64;
+  uint32_t mask[TPL];
+#pragma unroll
+  for (int c = 0; c < TPL; ++c) {
+    const int t = c * 64 + lane;
+    mask[c] = t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
+  }
+  int my_cnt = 0, my_off = 0, total = 0;
+  for (int e2 = 0; e2 < e_local; ++e2) {
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < TPL; ++c) n += __popcll(__ballot((mask[c] >> e2) & 1u));
+    if (e2 < e) my_off += n;
+    if (e2 == e) my_cnt = n;
+    if (blockIdx.x == 0 && lane == 0) { counts[e2] = n; offsets[e2] = total; }
+    total += n;
+  }
+  if (blockIdx.x == 0) {
+    if (lane == 0) offsets[e_local] = total;
+#pragma unroll
+    for (int c = 0; c < TPL; ++c) {
+      const int t = c * 64 + lane;
+      if (t < T)
+        for (int k = __popc(mask[c]); k < TOP_K; ++k) token_route[(size_t)t * TOP_K + k] = -1;
+    }
+  }
+  if (my_cnt == 0) return;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int base = 0;
+#pragma unroll
+  for (int c = 0; c < TPL; ++c) {
+    const int t = c * 64 + lane;
+    const bool hit = (mask[c] >> e) & 1u;
+    const uint64_t bal = __ballot(hit);
+    if (hit) {
+      const int slot = base + __popcll(bal & below);
+      s_tok[slot] = t;
+      if (j == 0) {
+        const int r = my_off + slot;
+        const int32_t* ids = topk_ids + (size_t)t * TOP_K;
+        int kpos = 0;
+#pragma unroll
+        for (int k = 0; k < TOP_K; ++k) kpos = (ids[k] == e + offset) ? k : kpos;
+        route_token[r] = t;
+        route_weight[r] = topk_w[(size_t)t * TOP_K + kpos];
+        token_route[(size_t)t * TOP_K + __popc(mask[c] & ((1u << e) - 1u))] = r;
+      }
+    }
+    base += __popcll(bal);
+  }
+  __syncthreads();
+
+  // ---- GEMM1 + SwiGLU for 16-route tiles
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  const int col = lane & 15;
+  const int nb = j >> 3, pj = j & 7;
+  const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(2 * pj) * TILE_BYTES;
+  const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
+  const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
+  for (int m0 = 0; m0 < my_cnt; m0 += BM) {
+    __asm__ volatile("" ::: "memory");  // keep the weight prologue inside the loop
+    const int rows = min(BM, my_cnt - m0);
+    const int tok = s_tok[m0 + (col < rows ? col : 0)];  // padding columns reuse a real row
+    const uint8_t* arow = hidden + (size_t)tok * H + 32 * (lane >> 4);
+    const float* srow = hscale + tok;
+    v8i wg[NR], wu[NR], bq[NR];
+    float as[NR];
+    auto issue = [&](int kb, int sl) {
+      const uint8_t* pw = wp + (size_t)kb * W13_KB_BYTES;
+      wg[sl] = load_tile_frag(pw, lane);
+      wu[sl] = load_tile_frag(pw + TILE_BYTES, lane);
+      const uint8_t* a = arow + kb * BLK;
+      bq[sl] = make_v8i(*reinterpret_cast<const uint4*>(a), *reinterpret_cast<const uint4*>(a + 16));
+      as[sl] = srow[(size_t)kb * T];
+    };
+#pragma unroll
+    for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
+    v4f accg = zero4, accu = zero4;
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < HB; kb0 += NR) {
+#pragma unroll
+      for (int sl = 0; sl < NR; ++sl) {
+        const int kb = kb0 + sl;
+        issue(min(kb + NR - 1, HB - 1), (sl + NR - 1) % NR);  // branch-free; the tail re-reads a K-block
+        __builtin_amdgcn_sched_barrier(0);
+        accg += mfma_16x16x128_fp8(wg[sl], bq[sl], zero4) * (as[sl] * wsg_p[kb]);
+        accu += mfma_16x16x128_fp8(wu[sl], bq[sl], zero4) * (as[sl] * wsu_p[kb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (col < rows) {
+      float4 c;
+      c.x = (accu[0] / (1.0f + __expf(-accu[0]))) * accg[0];
+      c.y = (accu[1] / (1.0f + __expf(-accu[1]))) * accg[1];
+      c.z = (accu[2] / (1.0f + __expf(-accu[2]))) * accg[2];
+      c.w = (accu[3] / (1.0f + __expf(-accu[3]))) * accg[3];
+      *reinterpret_cast<float4*>(Cf + (size_t)(my_off + m0 + col) * I + 16 * j + 4 * (lane >> 4)) = c;
+    }
+  }
+}
+
+// FP8 requant of the decode path's SwiGLU output: per (route, 128-column
+// block) scale = max(amax/448, 1e-8), C = e4m3(c / scale) (kernels/moe.cu:516-541).
+// 16 threads per block, 8 columns each.
+__global__ void __launch_bounds__(256)
+quant_kernel(const float* __restrict__ Cf, const int32_t* __restrict__ offsets, int e_local,
+             uint8_t* __restrict__ Cq, float* __restrict__ Cs) {
+  const int R = offsets[e_local];
+  const int tid = threadIdx.x, blk = tid >> 4, sub = tid & 15;
+  for (int r = blockIdx.x; r < R; r += gridDim.x) {
+    const float* src = Cf + (size_t)r * I + blk * BLK + sub * 8;
+    const float4 a = reinterpret_cast<const float4*>(src)[0];
+    const float4 b = reinterpret_cast<const float4*>(src)[1];
+    float m = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                    fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    const float sc = fmaxf(m / E4M3_MAX, 1.0e-8f);
+    auto q = [&](float x) { return fminf(fmaxf(x / sc, -E4M3_MAX), E4M3_MAX); };
+    uint2 o;
+    o.x = cvt2_e4m3(q(a.x), q(a.y)) | (cvt2_e4m3(q(a.z), q(a.w)) << 16);
+    o.y = cvt2_e4m3(q(b.x), q(b.y)) | (cvt2_e4m3(q(b.z), q(b.w)) << 16);
+    *reinterpret_cast<uint2*>(Cq + (size_t)r * I + blk * BLK + sub * 8) = o;
+    if (sub == 0) Cs[(size_t)r * IB + blk] = sc;
+  }
+}
+
+// Stage 2, one wave per (expert e, 64-row H slice q): tiles 4*(q%2)..+3 of
+// the 128-row slab hb = q/2.
+template <int NR>
+__global__ void __launch_bounds__(64)
+stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
+                     const float* __restrict__ w2s, const int32_t* __restrict__ counts,
+                     const int32_t* __restrict__ offsets, const float* __restrict__ route_weight,
+                     float* __restrict__ Y, int e_local) {
+  constexpr int BM = 16, NSLICE = H / 64;
+  static_assert(IB % NR == 0, "ring depth must divide the K-block count");
+  const int lane = threadIdx.x;
+  int e, q;
+  decode_map(blockIdx.x, NSLICE, e, q);
+  if (e >= e_local) return;
+  const int cnt = counts[e];
+  if (cnt == 0) return;
+  const int off = offsets[e];
+  const int hb = q >> 1, t0 = 4 * (q & 1);
+  const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
+  const float* ws_p = w2s + (size_t)(e * HB + hb) * IB;
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  const int col = lane & 15;
+
+  for (int m0 = 0; m0 < cnt; m0 += BM) {
+    __asm__ volatile("" ::: "memory");  // keep the weight prologue inside the loop
+    const int rows = min(BM, cnt - m0);
+    const int rb = off + m0;
+    const int r = rb + (col < rows ? col : 0);
+    const uint8_t* arow = Cq + (size_t)r * I + 32 * (lane >> 4);
+    const float* srow = Cs + (size_t)r * IB;
+    v8i wt[NR][4], bq[NR];
+    float as[NR];
+    auto issue = [&](int kb, int sl) {
+      const uint8_t* pw = wp + (size_t)kb * W2_KB_BYTES;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wt[sl][i] = load_tile_frag(pw + i * TILE_BYTES, lane);
+      const uint8_t* a = arow + kb * BLK;
+      bq[sl] = make_v8i(*reinterpret_cast<const uint4*>(a), *reinterpret_cast<const uint4*>(a + 16));
+      as[sl] = srow[kb];
+    };
+#pragma unroll
+    for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
+    v4f acc[4] = {zero4, zero4, zero4, zero4};
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < IB; kb0 += NR) {
+#pragma unroll
+      for (int sl = 0; sl < NR; ++sl) {
+        const int kb = kb0 + sl;
+        issue(min(kb + NR - 1, IB - 1), (sl + NR - 1) % NR);  // branch-free, clamped
+        const float sc = as[sl] * ws_p[kb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_barrier(0);
+          acc[i] += mfma_16x16x128_fp8(wt[sl][i], bq[sl], zero4) * sc;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (col < rows) {
+      const float rw = route_weight[rb + col];
+      float* yrow = Y + (size_t)(rb + col) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v4f y = acc[i] * rw;
+        *reinterpret_cast<float4*>(yrow + 16 * i) = make_float4(y[0], y[1], y[2], y[3]);
+      }
+    }
   }
 }
 
@@ -468,17 +708,39 @@ hipError_t run_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, co
   return hipGetLastError();
 }
 
-// Small batches stream weights with 16-route tiles; larger ones reuse each
-// weight fragment across 128 routes.
-constexpr int kSmallRoutes = 4096;
-
 }  // namespace
+
+hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
+                                const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
+                                const float* w13_scale, int32_t* counts, int32_t* offsets, int32_t* route_token,
+                                float* route_weight, int32_t* token_route, float* Cf, uint8_t* Cq, float* Cs,
+                                hipStream_t stream) {
+  if (T > DECODE_MAX_T) return hipErrorInvalidValue;
+  const int grid = e_local * (I / 16);
+  stage1_decode_kernel<4><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale, w13p,
+                                                   w13_scale, counts, offsets, route_token, route_weight, token_route,
+                                                   Cf);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  const int R = T * (e_local < TOP_K ? e_local : TOP_K);
+  quant_kernel<<<R < 1024 ? (R > 0 ? R : 1) : 1024, 256, 0, stream>>>(Cf, offsets, e_local, Cq, Cs);
+  return hipGetLastError();
+}
+
+hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
+                                const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
+                                int e_local, hipStream_t stream) {
+  const int grid = e_local * (H / 64);
+  stage2_decode_kernel<4><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
+                                                   e_local);
+  return hipGetLastError();
+}
 
 hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local, int max_routes,
                          hipStream_t stream) {
-  if (max_routes <= kSmallRoutes)
+  if (max_routes <= 4096)
     return run_stage1<8, 1, 4>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
                                e_local, max_routes, stream);
   return run_stage1<4, 8, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
@@ -489,7 +751,7 @@ hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
                          int T, int e_local, int max_routes, hipStream_t stream) {
   (void)T;
-  if (max_routes <= kSmallRoutes)
+  if (max_routes <= 4096)
     return run_stage2<8, 1, 4>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
                                stream);
   return run_stage2<4, 8, 2>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,

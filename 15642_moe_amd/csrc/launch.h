@@ -29,6 +29,17 @@ hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
                          float* Y, int T, int e_local, int max_routes, hipStream_t stream);
 
+// Decode path (T <= DECODE_MAX_T): GEMM1 + SwiGLU with the local dispatch
+// fused in (fp32 output Cf), the FP8 requant, then GEMM2 over 64-row items.
+hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
+                                const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
+                                const float* w13_scale, int32_t* counts, int32_t* offsets, int32_t* route_token,
+                                float* route_weight, int32_t* token_route, float* Cf, uint8_t* Cq, float* Cs,
+                                hipStream_t stream);
+hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
+                                const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
+                                int e_local, hipStream_t stream);
+
 hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n, hipStream_t stream);
 
 }  // namespace moe

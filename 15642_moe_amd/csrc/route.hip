@@ -4,7 +4,8 @@
 //                    (semantics of reference/moe_ref.py:81-107; the reference
 //                    kernel is route_dispatch_kernel, kernels/moe.cu:213-329).
 // dispatch_kernel  : deterministic token-ordered compaction of the local
-//                    (token, expert) pairs into per-expert route lists.
+//                    (token, expert) pairs into per-expert route lists, one
+//                    workgroup per 256-token chunk.
 // combine_kernel   : per-token sum of the weighted per-route expert outputs in
 //                    ascending expert order, then bf16 RNE (the reference does
 //                    fp32 atomics + bf16_convert_kernel, kernels/moe.cu:682,688-695;
@@ -22,20 +23,27 @@ __device__ __forceinline__ float sigmoid_cr(float x) {
   return __fdiv_rn(1.0f, d);
 }
 
-// Max of (value, index) pairs ordered by value descending, then index ascending.
-__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
-  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+// Order-preserving map of a (non-NaN) float to uint32; 0 sits below every
+// finite value and marks excluded candidates.
+__device__ __forceinline__ uint32_t order_key(float v) {
+  const uint32_t b = __float_as_uint(v);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+
+__device__ __forceinline__ int popc(uint64_t m) { return __popcll(m); }
 
 __global__ void __launch_bounds__(256)
 route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, float rsf, int T,
              int32_t* __restrict__ topk_ids, float* __restrict__ topk_w) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;  // uniform per wave
+  __shared__ float s_sel[4][TOP_K];
+  __shared__ int s_id[4][TOP_K];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  const bool active = t < T;  // uniform per wave; idle waves still reach the barrier
+  const int tt = active ? t : 0;
 
   // Lane l owns experts 4l..4l+3; group g = lanes 8g..8g+7.
-  const float4 x4 = reinterpret_cast<const float4*>(logits + (size_t)t * E_GLOBAL)[lane];
+  const float4 x4 = reinterpret_cast<const float4*>(logits + (size_t)tt * E_GLOBAL)[lane];
   const float4 b4 = reinterpret_cast<const float4*>(bias)[lane];
   float s[4], v[4];
   s[0] = sigmoid_cr(x4.x); s[1] = sigmoid_cr(x4.y); s[2] = sigmoid_cr(x4.z); s[3] = sigmoid_cr(x4.w);
@@ -67,182 +75,179 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   }
   const bool group_sel = rank < TOPK_GROUP;
 
-  float cand[4];
+  // Top-8 experts of the kept groups by (value desc, index asc): the 8th
+  // largest key is found bit by bit from wave-wide ballot counts, then ties
+  // at that key are filled in ascending expert order.
+  uint32_t key[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) cand[j] = group_sel ? v[j] : -INFINITY;
-
-  // Top-8 experts by (biased score desc, index asc) over the selected groups.
-  int pid[TOP_K];
-  float ps[TOP_K];
+  for (int j = 0; j < 4; ++j) key[j] = group_sel ? order_key(v[j]) : 0u;
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-  for (int k = 0; k < TOP_K; ++k) {
-    float bv = cand[0];
-    int bi = lane * 4;
+    for (int j = 0; j < 4; ++j) cnt += popc(__ballot(key[j] >= cand));
+    if (cnt >= TOP_K) thr = cand;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int n_gt = 0, eq_seen = 0;
 #pragma unroll
-    for (int j = 1; j < 4; ++j)
-      if (cand[j] > bv) { bv = cand[j]; bi = lane * 4 + j; }
+  for (int j = 0; j < 4; ++j) {
+    n_gt += popc(__ballot(key[j] > thr));
+    eq_seen += popc(__ballot(key[j] == thr) & below);
+  }
+  const int need = TOP_K - n_gt;
+  bool sel[4];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
-      argmax_merge(bv, bi, ov, oi);
-    }
-    const int owner = bi >> 2, slot = bi & 3;
-    float my_s = s[0];
+  for (int j = 0; j < 4; ++j) {
+    const bool eq = key[j] == thr;
+    sel[j] = key[j] > thr || (eq && eq_seen < need);
+    eq_seen += eq ? 1 : 0;
+  }
+  // Position in ascending expert order = selected experts below this one.
+  int pos = 0;
 #pragma unroll
-    for (int j = 1; j < 4; ++j) my_s = (slot == j) ? s[j] : my_s;
-    ps[k] = __shfl(my_s, owner);
-    pid[k] = bi;
-    if (lane == owner) {
+  for (int j = 0; j < 4; ++j) pos += popc(__ballot(sel[j]) & below);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (j == slot) cand[j] = -INFINITY;
+  for (int j = 0; j < 4; ++j) {
+    if (sel[j]) {
+      s_sel[wave][pos] = s[j];
+      s_id[wave][pos] = lane * 4 + j;
+      ++pos;
     }
   }
-
-  // Ascending expert order (fixes the weight-sum and combine order).
-#pragma unroll
-  for (int a = 1; a < TOP_K; ++a) {
-#pragma unroll
-    for (int b = a; b > 0; --b) {
-      if (pid[b] < pid[b - 1]) {
-        const int ti = pid[b]; pid[b] = pid[b - 1]; pid[b - 1] = ti;
-        const float tf = ps[b]; ps[b] = ps[b - 1]; ps[b - 1] = tf;
-      }
-    }
-  }
+  __syncthreads();
+  // Ascending-expert-order sum fixes the rounding of the denominator.
   float sum = 0.0f;
 #pragma unroll
-  for (int k = 0; k < TOP_K; ++k) sum += ps[k];
+  for (int k = 0; k < TOP_K; ++k) sum += s_sel[wave][k];
   sum += 1e-20f;
-
-  if (lane < TOP_K) {
-    int id = pid[0];
-    float sv = ps[0];
-#pragma unroll
-    for (int k = 1; k < TOP_K; ++k)
-      if (lane == k) { id = pid[k]; sv = ps[k]; }
-    topk_ids[(size_t)t * TOP_K + lane] = id;
-    topk_w[(size_t)t * TOP_K + lane] = __fdiv_rn(sv, sum) * rsf;
+  if (active && lane < TOP_K) {
+    topk_ids[(size_t)t * TOP_K + lane] = s_id[wave][lane];
+    topk_w[(size_t)t * TOP_K + lane] = __fdiv_rn(s_sel[wave][lane], sum) * rsf;
   }
 }
 
-// Bit le of the result is set when the token picked global expert le+offset.
-__device__ __forceinline__ uint32_t local_mask(const int32_t* ids, int offset, int e_local) {
-  uint32_t m = 0;
-#pragma unroll
-  for (int k = 0; k < TOP_K; ++k) {
-    const int le = ids[k] - offset;
-    if (le >= 0 && le < e_local) m |= 1u << le;
-  }
-  return m;
-}
+// One workgroup per chunk of 256 tokens.  Each workgroup histograms the local
+// picks of all tokens (those before its chunk give its per-expert base) and
+// then ranks its own tokens per expert with wave ballots, so slots follow token
+// order (a stable counting sort) and the dispatch is deterministic.  Route r
+// of expert e lives at offsets[e] + slot.
+constexpr int DISPATCH_CHUNK = 256;
 
-// Single workgroup: pass 1 counts routes per local expert, pass 2 assigns
-// slots in token order (stable counting sort), so the dispatch is
-// deterministic.  Route r of expert e lives at offsets[e] + slot.
-__global__ void __launch_bounds__(1024)
+__global__ void __launch_bounds__(DISPATCH_CHUNK)
 dispatch_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T,
                 int e_local, int offset, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                 int32_t* __restrict__ route_token, float* __restrict__ route_weight,
                 int32_t* __restrict__ token_route) {
-  __shared__ int s_cnt[MAX_E_LOCAL], s_base[MAX_E_LOCAL];
-  __shared__ int s_wtot[16][MAX_E_LOCAL], s_woff[16][MAX_E_LOCAL];
+  constexpr int NWAVE = DISPATCH_CHUNK / 64;
+  __shared__ int s_pre[NWAVE][MAX_E_LOCAL], s_tot[NWAVE][MAX_E_LOCAL];
+  __shared__ int s_base[MAX_E_LOCAL];
+  __shared__ int s_wtot[NWAVE][MAX_E_LOCAL], s_woff[NWAVE][MAX_E_LOCAL];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < MAX_E_LOCAL) s_cnt[tid] = 0;
+  const int c0 = blockIdx.x * DISPATCH_CHUNK;
+  if (tid < MAX_E_LOCAL) {
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) { s_pre[w][tid] = 0; s_tot[w][tid] = 0; }
+  }
   __syncthreads();
-  for (int t = tid; t < T; t += 1024) {
+  for (int t = tid; t < T; t += DISPATCH_CHUNK) {
     uint32_t m = local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local);
     while (m) {
       const int e = __builtin_ctz(m);
       m &= m - 1;
-      atomicAdd(&s_cnt[e], 1);
+      atomicAdd(&s_tot[wave][e], 1);
+      if (t < c0) atomicAdd(&s_pre[wave][e], 1);
     }
+  }
+  __syncthreads();
+  if (tid < MAX_E_LOCAL) {
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) { pre += s_pre[w][tid]; tot += s_tot[w][tid]; }
+    s_pre[0][tid] = pre;
+    s_tot[0][tid] = tot;
   }
   __syncthreads();
   if (tid == 0) {
     int acc = 0;
     for (int e = 0; e < e_local; ++e) {
-      s_base[e] = acc;
-      counts[e] = s_cnt[e];
-      offsets[e] = acc;
-      acc += s_cnt[e];
+      s_base[e] = acc + s_pre[0][e];
+      if (blockIdx.x == 0) { counts[e] = s_tot[0][e]; offsets[e] = acc; }
+      acc += s_tot[0][e];
     }
-    offsets[e_local] = acc;
+    if (blockIdx.x == 0) offsets[e_local] = acc;
+  }
+
+  const int t = c0 + tid;
+  const bool valid = t < T;
+  int ids[TOP_K];
+  float ws[TOP_K];
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k) {
+    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
+    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
+  }
+  const uint32_t m = valid ? local_mask(ids, offset, e_local) : 0u;
+  for (int e = 0; e < e_local; ++e) {
+    const uint64_t bal = __ballot((m >> e) & 1u);
+    if (lane == 0) s_wtot[wave][e] = __popcll(bal);
   }
   __syncthreads();
-
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int c0 = 0; c0 < T; c0 += 1024) {
-    const int t = c0 + tid;
-    const bool valid = t < T;
-    int ids[TOP_K];
-    float ws[TOP_K];
+  if (tid < e_local) {
+    int acc = 0;
 #pragma unroll
-    for (int k = 0; k < TOP_K; ++k) {
-      ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
-      ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
-    }
-    const uint32_t m = valid ? local_mask(ids, offset, e_local) : 0u;
-    for (int e = 0; e < e_local; ++e) {
-      const uint64_t bal = __ballot((m >> e) & 1u);
-      if (lane == 0) s_wtot[wave][e] = __popcll(bal);
-    }
-    __syncthreads();
-    if (tid < e_local) {
-      int acc = 0;
-      for (int w = 0; w < 16; ++w) {
-        s_woff[w][tid] = acc;
-        acc += s_wtot[w][tid];
-      }
-    }
-    __syncthreads();
-    int j = 0;
-    for (int e = 0; e < e_local; ++e) {
-      const uint64_t bal = __ballot((m >> e) & 1u);
-      if ((m >> e) & 1u) {
-        const int r = s_base[e] + s_woff[wave][e] + __popcll(bal & lt_mask);
-        float wsel = 0.0f;
-#pragma unroll
-        for (int k = 0; k < TOP_K; ++k)
-          if (ids[k] - offset == e) wsel = ws[k];
-        route_token[r] = t;
-        route_weight[r] = wsel;
-        token_route[(size_t)t * TOP_K + j] = r;
-        ++j;
-      }
-    }
-    if (valid)
-      for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
-    __syncthreads();
-    if (tid < e_local) s_base[tid] += s_woff[15][tid] + s_wtot[15][tid];
-    __syncthreads();
+    for (int w = 0; w < NWAVE; ++w) { s_woff[w][tid] = acc; acc += s_wtot[w][tid]; }
   }
+  __syncthreads();
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int j = 0;
+  for (int e = 0; e < e_local; ++e) {
+    const uint64_t bal = __ballot((m >> e) & 1u);
+    if ((m >> e) & 1u) {
+      const int r = s_base[e] + s_woff[wave][e] + __popcll(bal & lt_mask);
+      float wsel = 0.0f;
+#pragma unroll
+      for (int k = 0; k < TOP_K; ++k)
+        if (ids[k] - offset == e) wsel = ws[k];
+      route_token[r] = t;
+      route_weight[r] = wsel;
+      token_route[(size_t)t * TOP_K + j] = r;
+      ++j;
+    }
+  }
+  if (valid)
+    for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
 }
 
-// out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] )
+// out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ).
+// Workgroup (t, part) covers 256 float4 columns of token t; the token's route
+// rows are loaded before any is used, so a launch costs one memory latency.
+constexpr int COMBINE_PARTS = H / 4 / 256;  // 7
+
 __global__ void __launch_bounds__(256)
 combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_route, int T,
                uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
-  if (t >= T) return;
-  int r[TOP_K];
+  const int i = blockIdx.y * 256 + threadIdx.x;  // float4 column
+  int r[TOP_K], n = 0;
 #pragma unroll
-  for (int k = 0; k < TOP_K; ++k) r[k] = token_route[(size_t)t * TOP_K + k];
-  for (int i = threadIdx.x; i < H / 4; i += 256) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < TOP_K; ++k) {
-      if (r[k] >= 0) {
-        const float4 y = reinterpret_cast<const float4*>(Y + (size_t)r[k] * H)[i];
-        acc.x += y.x; acc.y += y.y; acc.z += y.z; acc.w += y.w;
-      }
-    }
-    uint2 o;
-    o.x = (uint32_t)bf16_rne(acc.x) | ((uint32_t)bf16_rne(acc.y) << 16);
-    o.y = (uint32_t)bf16_rne(acc.z) | ((uint32_t)bf16_rne(acc.w) << 16);
-    reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = o;
+  for (int k = 0; k < TOP_K; ++k) {
+    r[k] = token_route[(size_t)t * TOP_K + k];
+    n += r[k] >= 0 ? 1 : 0;  // valid routes come first
   }
+  float4 y[TOP_K];
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k)
+    if (k < n) y[k] = reinterpret_cast<const float4*>(Y + (size_t)r[k] * H)[i];
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k)
+    if (k < n) { acc.x += y[k].x; acc.y += y[k].y; acc.z += y[k].z; acc.w += y[k].w; }
+  uint2 o;
+  o.x = (uint32_t)bf16_rne(acc.x) | ((uint32_t)bf16_rne(acc.y) << 16);
+  o.y = (uint32_t)bf16_rne(acc.z) | ((uint32_t)bf16_rne(acc.w) << 16);
+  reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = o;
 }
 
 hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
@@ -255,15 +260,16 @@ hipError_t launch_route(const float* logits, const float* bias, float rsf, int T
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, hipStream_t stream) {
-  dispatch_kernel<<<1, 1024, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, counts, offsets,
-                                          route_token, route_weight, token_route);
+  const int grid = T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1;
+  dispatch_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, counts, offsets,
+                                                       route_token, route_weight, token_route);
   return hipGetLastError();
 }
 
 hipError_t launch_combine(const float* Y, const int32_t* token_route, int T, uint16_t* out,
                           hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  combine_kernel<<<T, 256, 0, stream>>>(Y, token_route, T, out);
+  combine_kernel<<<dim3(T, COMBINE_PARTS), 256, 0, stream>>>(Y, token_route, T, out);
   return hipGetLastError();
 }
 
