@@ -22,7 +22,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "lib15642_moe_fp8.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["route.hip", "pack.hip", "gemm.hip", "capi.hip"]
+SOURCES = ["route.hip", "pack.hip", "gemm.hip", "prefill.hip", "capi.hip"]
 ARCH = "gfx950"
 
 
@@ -42,6 +42,9 @@ def compile_flags() -> list[str]:
         "-Wall",
         "-Wno-unused-result",
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA results in VGPRs: the per-K-block scale FMAs read them directly
+        # instead of through v_accvgpr_read copies.
+        "-mllvm", "-amdgpu-mfma-vgpr-form=1",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
     ]

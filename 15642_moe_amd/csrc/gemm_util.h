@@ -1,0 +1,105 @@
+// Helpers shared by the decode and prefill grouped-GEMM translation units.
+#pragma once
+
+#include "common.h"
+
+#include <mutex>
+
+namespace moe {
+
+__device__ __forceinline__ v8i make_v8i(const uint4& lo, const uint4& hi) {
+  v8i r;
+  r[0] = (int)lo.x; r[1] = (int)lo.y; r[2] = (int)lo.z; r[3] = (int)lo.w;
+  r[4] = (int)hi.x; r[5] = (int)hi.y; r[6] = (int)hi.z; r[7] = (int)hi.w;
+  return r;
+}
+
+// 32-byte operand fragment of one 2 KB tile in split-half layout:
+// half h of lane l at h*1024 + l*16 (global or LDS).
+__device__ __forceinline__ v8i load_tile_frag(const uint8_t* __restrict__ tile, int lane) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(tile + lane * 16);
+  const uint4 hi = *reinterpret_cast<const uint4*>(tile + 1024 + lane * 16);
+  return make_v8i(lo, hi);
+}
+
+// Slot -> logical work index.  Workgroup p always runs on XCD p % 8; within
+// each round of G slots, XCD x receives a contiguous run of logical works, so
+// the route tiles and weight blocks that share data run on one XCD (and its
+// L2) at the same time.
+__device__ __forceinline__ int xcd_logical(int slot, int G, int n_work) {
+  const int round0 = slot - slot % G;
+  const int p = slot - round0;
+  const int n_rem = min(G, n_work - round0);
+  const int x = p & 7, q = p >> 3;
+  const int base = n_rem >> 3, extra = n_rem & 7;
+  return round0 + x * base + min(x, extra) + q;
+}
+
+// Per-workgroup table of route tiles per local expert: expert e owns route
+// tiles s_tp[e] .. s_tp[e+1]-1 of BM routes each.
+template <int BM>
+__device__ __forceinline__ void load_tile_table(const int32_t* __restrict__ counts,
+                                                const int32_t* __restrict__ offsets, int e_local, int* s_tp,
+                                                int* s_cnt, int* s_off) {
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int e = 0; e < e_local; ++e) {
+      const int c = counts[e];
+      s_cnt[e] = c;
+      s_off[e] = offsets[e];
+      s_tp[e] = acc;
+      acc += (c + BM - 1) / BM;
+    }
+    s_tp[e_local] = acc;
+  }
+  __syncthreads();
+}
+
+// Logical work L -> (expert, weight block, route tile); works are ordered
+// expert-major, then weight block, then route tile, so the route tiles that
+// read one weight block are neighbours (same XCD, same round: the block is
+// fetched from HBM once and re-read from L2).
+__device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const int* s_tp, int& e, int& blk,
+                                            int& mt) {
+  e = 0;
+  while (e + 1 < e_local && s_tp[e + 1] * nblk <= L) ++e;
+  const int ntile = s_tp[e + 1] - s_tp[e];
+  const int local = L - s_tp[e] * nblk;
+  blk = local / ntile;
+  mt = local - blk * ntile;
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+
+// Compute units of the current device (cached per device).
+inline int device_cus() {
+  static std::mutex mu;
+  static int cus_of[64] = {0};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lk(mu);
+  int& c = cus_of[dev & 63];
+  if (c == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    c = cus;
+  }
+  return c;
+}
+
+template <typename K>
+int resident_blocks(K kernel, int threads) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess || per_cu <= 0)
+    per_cu = 1;
+  return per_cu * device_cus();
+}
+
+inline int persistent_grid(long long work_bound, int resident) {
+  const long long g = work_bound < resident ? work_bound : resident;
+  return (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace moe

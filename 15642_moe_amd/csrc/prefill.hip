@@ -1,0 +1,433 @@
+// Prefill-path grouped FP8 GEMMs (T > DECODE_MAX_T) on
+// v_mfma_f32_16x16x128_f8f6f4.
+//
+// stage1_tile_kernel : G = A_e x W13_e^T with per-128-K block scales
+//     hidden_scale[kb, tok] * W13_scale[e, nb or 16+nb, kb]
+//     (kernels/moe.cu:338-542, reference/moe_ref.py:58-73,128), SwiGLU
+//     c = gate * silu(up) (moe_ref.py:129-130) and the per-(route, 128-I-block)
+//     FP8 requant C = e4m3(c / max(amax/448, 1e-8)) (moe.cu:516-541).
+// stage2_tile_kernel : O = C x W2_e^T with C_scale x W2 block scales
+//     (moe.cu:547-686, moe_ref.py:75-79,131), Y = O * routing weight.
+//
+// Work item = (expert, 256 weight rows, tile of BM = 16*CT routes).  The 8
+// waves of a workgroup split it 4 x 2: wave (wr, wc) owns 4 weight tiles
+// (64 rows) x CT/2 route tiles, so one wave's accumulators are 4*CT/2 MFMA
+// tiles.  Weights are the MFMA A operand and stream from HBM straight into a
+// four-slot register ring, two K-blocks ahead.  Routed activations are the B
+// operand: each K-block of the route tile is gathered into registers three
+// steps ahead (two staging sets), then written to one of two LDS buffers in the fragment layout (XOR-swizzled so
+// both the stores and the fragment reads are free of bank conflicts) and
+// read by the four row groups.  Every load goes to registers, so all waits
+// are the compiler's own in-order vmcnt waits; one barrier per K-block.
+#include "common.h"
+#include "gemm_util.h"
+#include "launch.h"
+
+namespace moe {
+namespace {
+
+constexpr int TW = 8;  // waves per workgroup (4 weight-row groups x 2 route halves)
+constexpr int TNT = TW * 64;
+
+template <int CT, int RW>
+struct TileGeom {
+  static constexpr int BM = 16 * CT;               // routes per tile
+  static constexpr int WT = 16 / RW;               // weight tiles per wave (16 per 256-row item)
+  static constexpr int CG = TW / RW;               // route groups
+  static constexpr int CW = CT / CG;               // route tiles per wave
+  static constexpr int NCH = BM * 8;               // 16-byte chunks per K-block of the route tile
+  static constexpr int ACH = (NCH + TNT - 1) / TNT;
+  static_assert((RW == 4 || RW == 8) && CT % CG == 0 && CT <= 16, "tile shape");
+  static_assert(BM <= TNT, "one scale per thread");
+};
+
+// LDS layout of the activation stages: s_act[route tile c][buffer][2 KB]
+// fragment tiles, s_scl[buffer][BM] scales.  In a fragment tile, chunk
+// (route i, lane-group g, half h) sits at h*1024 + (g*16 + (i ^ 4g))*16:
+// lane l reads route l%16, group l/16, so each half is a permutation of the
+// 64 16-byte slots (conflict-free reads), and one lane offset serves both
+// halves and every (tile, buffer) through the instruction's immediate offset
+// (c*4096 + buffer*2048 + h*1024 < 64 KB for CT <= 16).
+__device__ __forceinline__ int frag_slot(int i, int g, int h) { return h * 1024 + (g * 16 + (i ^ (g << 2))) * 16; }
+
+__device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
+  const uint4 lo = *reinterpret_cast<const uint4*>(p);
+  const uint4 hi = *reinterpret_cast<const uint4*>(p + 1024);
+  return make_v8i(lo, hi);
+}
+
+// Registers holding one K-block of the route tile on its way to LDS: this
+// thread's ACH 16-byte chunks (chunk x = tid + i*TNT: route x/8, K chunk x%8)
+// and, for tid < BM, route tid's activation scale.
+template <int CT, int RW>
+struct ActStage {
+  using G = TileGeom<CT, RW>;
+  uint4 v[G::ACH];
+  float sc;
+
+  // row r's K-block starts at abase + s_rowoff[r] + kofs; its scale at
+  // sbase + s_soff[r] + sofs.  Padding routes repeat route 0 (a real row).
+  __device__ __forceinline__ void load(const uint8_t* __restrict__ abase, const long long* s_rowoff, size_t kofs,
+                                       const float* __restrict__ sbase, const int* s_soff, size_t sofs, int tid) {
+#pragma unroll
+    for (int i = 0; i < G::ACH; ++i) {
+      const int x = tid + i * TNT;
+      v[i] = (G::NCH % TNT == 0 || x < G::NCH)
+                 ? *reinterpret_cast<const uint4*>(abase + s_rowoff[x >> 3] + kofs + (x & 7) * 16)
+                 : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < G::BM) sc = sbase[s_soff[tid] + sofs];
+  }
+
+  // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM].
+  __device__ __forceinline__ void store(uint8_t* s_act, float* s_scl, int b, int tid) const {
+#pragma unroll
+    for (int i = 0; i < G::ACH; ++i) {
+      const int x = tid + i * TNT;
+      if (G::NCH % TNT == 0 || x < G::NCH) {
+        const int r = x >> 3, q = x & 7;
+        *reinterpret_cast<uint4*>(s_act + ((r >> 4) * 2 + b) * TILE_BYTES + frag_slot(r & 15, q >> 1, q & 1)) = v[i];
+      }
+    }
+    if (tid < G::BM) s_scl[b * G::BM + tid] = sc;
+  }
+};
+
+// Per-step barrier: this wave's LDS stores are complete, then all waves meet.
+// Written as one statement so no VMEM wait is attached to it.
+__device__ __forceinline__ void step_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// One K-block of a wave's tile: acc[t][cc] += (W_t x B_cc) * (a_scale[cc] *
+// w_scale(t)) for its WT weight tiles (wf) and CW route tiles, B fragments
+// at af + cc*4096 and route scales at as_[cc*16] in LDS.  Software-pipelined
+// by one route tile: the scale FMAs of route tile cc-1 (whose MFMA results
+// are ready by then) run in the shadow of route tile cc's MFMAs instead of
+// stalling on them.  All CW route tiles are computed; padding routes hold a
+// copy of route 0 and their columns are never stored.
+template <int WT, int CW, typename WS>
+__device__ __forceinline__ void mma_step(v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af, const float* as_,
+                                         WS ws) {
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  float a[2];
+  v4f p[2][WT];
+#pragma unroll
+  for (int cc = 0; cc < CW; ++cc) {
+    const int cur = cc & 1;
+    __asm__ volatile("" ::: "memory");  // no speculative hoisting of later tiles' LDS reads
+    const v8i b = lds_frag(af + cc * 2 * TILE_BYTES);
+    a[cur] = as_[cc * 16];
+#pragma unroll
+    for (int t = 0; t < WT; ++t) p[cur][t] = mfma_16x16x128_fp8(wf[t], b, zero4);
+    if (cc > 0) {
+#pragma unroll
+      for (int t = 0; t < WT; ++t) acc[t][cc - 1] += p[cur ^ 1][t] * (a[cur ^ 1] * ws(t));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // one route tile per pipeline stage
+  }
+#pragma unroll
+  for (int t = 0; t < WT; ++t) acc[t][CW - 1] += p[(CW - 1) & 1][t] * (a[(CW - 1) & 1] * ws(t));
+}
+
+// ---------------------------------------------------------------------------
+// Stage 1.  Item (e, nb, mt): W13 rows of I-block nb (gate tiles 2j, up tiles
+// 2j+1, j = 0..7) x routes mt*BM...  Wave (wr, wc) owns weight tiles
+// wr*WT .. wr*WT+WT-1 (gate/up pairs j = wr*WT/2 ..) x route tiles
+// wc*CW .. wc*CW+CW-1.
+// ---------------------------------------------------------------------------
+template <int CT, int RW>
+__global__ void __launch_bounds__(TNT)
+stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
+                   const uint8_t* __restrict__ w13p, const float* __restrict__ w13s,
+                   const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
+                   const int32_t* __restrict__ route_token, uint8_t* __restrict__ Cq, float* __restrict__ Cs, int T,
+                   int e_local) {
+  using G = TileGeom<CT, RW>;
+  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2;
+  static_assert(HB % 4 == 0, "four-step unroll");
+  __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
+  __shared__ float s_scl[2 * BM];
+  __shared__ long long s_rowoff[BM];
+  __shared__ int s_soff[BM];
+  __shared__ float s_red[RW][BM];
+  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w % RW, wc = (RW == TW) ? 0 : w / RW;
+  load_tile_table<BM>(counts, offsets, e_local, s_tp, s_cnt, s_off);
+  const int n_work = s_tp[e_local] * IB;
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  for (int slot = blockIdx.x; slot < n_work; slot += gridDim.x) {
+    int e, nb, mt;
+    decode_work(xcd_logical(slot, gridDim.x, n_work), IB, e_local, s_tp, e, nb, mt);
+    const int m0 = mt * BM;
+    const int rows = min(BM, s_cnt[e] - m0);
+    const int rb = s_off[e] + m0;
+    for (int r = tid; r < BM; r += TNT) {
+      const int tok = route_token[rb + (r < rows ? r : 0)];
+      s_rowoff[r] = (long long)tok * H;
+      s_soff[r] = tok;
+    }
+    __syncthreads();
+
+    const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
+    const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
+    const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
+    // This lane's fragment / scale addresses in LDS for route tile wc*CW.
+    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
+    v8i wf[4][WT];
+    auto wload = [&](int sl, int kb) {
+#pragma unroll
+      for (int t = 0; t < WT; ++t) wf[sl][t] = load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane);
+    };
+    v4f acc[WT][CW];
+#pragma unroll
+    for (int t = 0; t < WT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+
+    // Pipeline: weights two K-blocks ahead (4-slot register ring), activations
+    // gathered three ahead into two staging sets and stored to LDS one ahead.
+    ActStage<CT, RW> st[2];
+    wload(0, 0);
+    wload(1, 1);
+    st[0].load(hidden, s_rowoff, 0, hscale, s_soff, 0, tid);
+    st[1].load(hidden, s_rowoff, BLK, hscale, s_soff, (size_t)T, tid);
+    st[0].store(s_act, s_scl, 0, tid);
+    st[0].load(hidden, s_rowoff, 2 * BLK, hscale, s_soff, 2 * (size_t)T, tid);
+
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < HB; kb0 += 4) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kb = kb0 + s;
+        step_barrier();  // stage kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
+        wload((s + 2) & 3, min(kb + 2, HB - 1));
+        st[(s + 1) & 1].store(s_act, s_scl, (s + 1) & 1, tid);  // stage kb+1 (past the end: dead copies)
+        const int ka = min(kb + 3, HB - 1);
+        st[(s + 1) & 1].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        const float wsg = wsg_p[kb], wsu = wsu_p[kb];
+        if (wc * CW * 16 < rows)  // route groups past the tile's routes skip the MFMAs
+          mma_step<WT, CW>(acc, wf[s], afrag + (s & 1) * TILE_BYTES, ascl + (s & 1) * BM,
+                           [&](int t) { return (t & 1) ? wsu : wsg; });
+      }
+    }
+
+    // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
+#pragma unroll
+    for (int jj = 0; jj < NP; ++jj)
+#pragma unroll
+      for (int cc = 0; cc < CW; ++cc)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float g = acc[2 * jj][cc][v], u = acc[2 * jj + 1][cc][v];
+          acc[2 * jj][cc][v] = (u / (1.0f + __expf(-u))) * g;
+        }
+    // Per-route amax over this wave's I columns, then over the RW row groups.
+#pragma unroll
+    for (int cc = 0; cc < CW; ++cc) {
+      float m = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < NP; ++jj)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(acc[2 * jj][cc][v]));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if (lane < 16) s_red[wr][(wc * CW + cc) * 16 + lane] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int cc = 0; cc < CW; ++cc) {
+      const int row = (wc * CW + cc) * 16 + (lane & 15);
+      if (row < rows) {
+        float am = s_red[0][row];
+#pragma unroll
+        for (int r2 = 1; r2 < RW; ++r2) am = fmaxf(am, s_red[r2][row]);
+        const float sc = fmaxf(am / E4M3_MAX, 1.0e-8f);
+        uint8_t* crow = Cq + (size_t)(rb + row) * I + nb * BLK + 4 * (lane >> 4);
+#pragma unroll
+        for (int jj = 0; jj < NP; ++jj) {
+          float q[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(acc[2 * jj][cc][v] / sc, -E4M3_MAX), E4M3_MAX);
+          const uint32_t packed = cvt2_e4m3(q[0], q[1]) | (cvt2_e4m3(q[2], q[3]) << 16);
+          *reinterpret_cast<uint32_t*>(crow + 16 * (wr * NP + jj)) = packed;
+        }
+        if (wr == 0 && lane < 16) Cs[(size_t)(rb + row) * IB + nb] = sc;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Stage 2.  Item (e, hp, mt): W2 rows 256*hp .. 256*hp+255 (H blocks 2hp and
+// 2hp+1, 16 row tiles) x routes mt*BM...  Wave (wr, wc) owns row tiles
+// wr*WT .. wr*WT+WT-1 x route tiles wc*CW ...  Y[r, h] = O[r, h] * weight[r].
+// ---------------------------------------------------------------------------
+template <int CT, int RW>
+__global__ void __launch_bounds__(TNT)
+stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
+                   const float* __restrict__ w2s, const int32_t* __restrict__ counts,
+                   const int32_t* __restrict__ offsets, const float* __restrict__ route_weight,
+                   float* __restrict__ Y, int e_local) {
+  using G = TileGeom<CT, RW>;
+  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2;
+  static_assert(IB % 4 == 0, "four-step unroll");
+  __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
+  __shared__ float s_scl[2 * BM];
+  __shared__ long long s_rowoff[BM];
+  __shared__ int s_soff[BM];
+  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wr = w % RW, wc = (RW == TW) ? 0 : w / RW;
+  load_tile_table<BM>(counts, offsets, e_local, s_tp, s_cnt, s_off);
+  const int n_work = s_tp[e_local] * NHP;
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+
+  for (int slot = blockIdx.x; slot < n_work; slot += gridDim.x) {
+    int e, hp, mt;
+    decode_work(xcd_logical(slot, gridDim.x, n_work), NHP, e_local, s_tp, e, hp, mt);
+    const int m0 = mt * BM;
+    const int rows = min(BM, s_cnt[e] - m0);
+    const int rb = s_off[e] + m0;
+    for (int r = tid; r < BM; r += TNT) {
+      const int rr = rb + (r < rows ? r : 0);
+      s_rowoff[r] = (long long)rr * I;
+      s_soff[r] = rr * IB;
+    }
+    __syncthreads();
+
+    const int g0 = wr * WT;  // first of this wave's 16 row tiles
+    const int hb = 2 * hp + (g0 >> 3), t0 = g0 & 7;
+    const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
+    const float* ws_p = w2s + (size_t)(e * HB + hb) * IB;
+    // This lane's fragment / scale addresses in LDS for route tile wc*CW.
+    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
+    v8i wf[4][WT];
+    auto wload = [&](int sl, int kb) {
+#pragma unroll
+      for (int t = 0; t < WT; ++t) wf[sl][t] = load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane);
+    };
+    v4f acc[WT][CW];
+#pragma unroll
+    for (int t = 0; t < WT; ++t)
+#pragma unroll
+      for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+
+    ActStage<CT, RW> st[2];
+    wload(0, 0);
+    wload(1, 1);
+    st[0].load(Cq, s_rowoff, 0, Cs, s_soff, 0, tid);
+    st[1].load(Cq, s_rowoff, BLK, Cs, s_soff, 1, tid);
+    st[0].store(s_act, s_scl, 0, tid);
+    st[0].load(Cq, s_rowoff, 2 * BLK, Cs, s_soff, 2, tid);
+
+#pragma unroll 1
+    for (int kb0 = 0; kb0 < IB; kb0 += 4) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int kb = kb0 + s;
+        step_barrier();
+        wload((s + 2) & 3, min(kb + 2, IB - 1));
+        st[(s + 1) & 1].store(s_act, s_scl, (s + 1) & 1, tid);
+        const int ka = min(kb + 3, IB - 1);
+        st[(s + 1) & 1].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        const float ws = ws_p[kb];
+        if (wc * CW * 16 < rows)
+          mma_step<WT, CW>(acc, wf[s], afrag + (s & 1) * TILE_BYTES, ascl + (s & 1) * BM, [&](int) { return ws; });
+      }
+    }
+
+#pragma unroll
+    for (int cc = 0; cc < CW; ++cc) {
+      const int row = (wc * CW + cc) * 16 + (lane & 15);
+      if (row < rows) {
+        const float rw = route_weight[rb + row];
+        float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+#pragma unroll
+        for (int t = 0; t < WT; ++t) {
+          const v4f y = acc[t][cc] * rw;
+          *reinterpret_cast<float4*>(yrow + 16 * t) = make_float4(y[0], y[1], y[2], y[3]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Tile shape for a launch from the expected routes per local expert
+// (T * 8 / 256 under uniform routing; skewed routing only adds tiles).
+enum TileShape { TILE_64x256, TILE_128x256, TILE_192x256 };
+TileShape tile_shape(int T) {
+  const int expected = T / 32;
+  return expected <= 64 ? TILE_64x256 : (expected <= 128 ? TILE_128x256 : TILE_192x256);
+}
+
+template <int CT, int RW>
+hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
+                           const int32_t* counts, const int32_t* offsets, const int32_t* route_token, uint8_t* Cq,
+                           float* Cs, int T, int e_local, int max_routes, hipStream_t stream) {
+  constexpr int BM = TileGeom<CT, RW>::BM;
+  auto k = stage1_tile_kernel<CT, RW>;
+  const long long bound = ((long long)e_local + max_routes / BM + 1) * IB;
+  const int grid = persistent_grid(bound, resident_blocks(k, TNT));
+  k<<<grid, TNT, 0, stream>>>(hidden, hs, w13p, w13s, counts, offsets, route_token, Cq, Cs, T, e_local);
+  return hipGetLastError();
+}
+
+template <int CT, int RW>
+hipError_t run_stage2_tile(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2s,
+                           const int32_t* counts, const int32_t* offsets, const float* rw, float* Y, int e_local,
+                           int max_routes, hipStream_t stream) {
+  constexpr int BM = TileGeom<CT, RW>::BM;
+  auto k = stage2_tile_kernel<CT, RW>;
+  const long long bound = ((long long)e_local + max_routes / BM + 1) * (HB / 2);
+  const int grid = persistent_grid(bound, resident_blocks(k, TNT));
+  k<<<grid, TNT, 0, stream>>>(Cq, Cs, w2p, w2s, counts, offsets, rw, Y, e_local);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
+                         const float* w13_scale, const int32_t* counts, const int32_t* offsets,
+                         const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local, int max_routes,
+                         hipStream_t stream) {
+  switch (tile_shape(T)) {
+    case TILE_64x256:
+      return run_stage1_tile<4, 4>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
+                                   e_local, max_routes, stream);
+    case TILE_128x256:
+      return run_stage1_tile<8, 4>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
+                                   e_local, max_routes, stream);
+    default:
+      return run_stage1_tile<12, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
+                                    e_local, max_routes, stream);
+  }
+}
+
+hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
+                         const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y, int T,
+                         int e_local, int max_routes, hipStream_t stream) {
+  switch (tile_shape(T)) {
+    case TILE_64x256:
+      return run_stage2_tile<4, 4>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
+                                   stream);
+    case TILE_128x256:
+      return run_stage2_tile<8, 4>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
+                                   stream);
+    default:
+      return run_stage2_tile<12, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
+                                    stream);
+  }
+}
+
+}  // namespace moe
