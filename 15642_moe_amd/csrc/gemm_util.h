@@ -55,18 +55,19 @@ __device__ __forceinline__ void load_tile_table(const int32_t* __restrict__ coun
   __syncthreads();
 }
 
-// Logical work L -> (expert, weight block, route tile); works are ordered
-// expert-major, then weight block, then route tile, so the route tiles that
-// read one weight block are neighbours (same XCD, same round: the block is
-// fetched from HBM once and re-read from L2).
+// Logical work L -> (expert, weight block, route tile).  Works are ordered
+// expert-major, then route tile, then weight block: the weight blocks that
+// read one route tile's activations are neighbours, so they run on one XCD
+// in the same round and the tile is fetched into that XCD's L2 once (the
+// activations are re-read by every weight block, the weights only by the
+// expert's few route tiles).
 __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const int* s_tp, int& e, int& blk,
                                             int& mt) {
   e = 0;
   while (e + 1 < e_local && s_tp[e + 1] * nblk <= L) ++e;
-  const int ntile = s_tp[e + 1] - s_tp[e];
   const int local = L - s_tp[e] * nblk;
-  blk = local / ntile;
-  mt = local - blk * ntile;
+  mt = local / nblk;
+  blk = local - mt * nblk;
 }
 
 // ---------------------------------------------------------------------------

@@ -10,15 +10,23 @@
 //     (moe.cu:547-686, moe_ref.py:75-79,131), Y = O * routing weight.
 //
 // Work item = (expert, 256 weight rows, tile of BM = 16*CT routes).  The 8
-// waves of a workgroup split it 4 x 2: wave (wr, wc) owns 4 weight tiles
-// (64 rows) x CT/2 route tiles, so one wave's accumulators are 4*CT/2 MFMA
-// tiles.  Weights are the MFMA A operand and stream from HBM straight into a
-// four-slot register ring, two K-blocks ahead.  Routed activations are the B
-// operand: each K-block of the route tile is gathered into registers three
-// steps ahead (two staging sets), then written to one of two LDS buffers in the fragment layout (XOR-swizzled so
-// both the stores and the fragment reads are free of bank conflicts) and
-// read by the four row groups.  Every load goes to registers, so all waits
-// are the compiler's own in-order vmcnt waits; one barrier per K-block.
+// waves of a workgroup split it RW x (8/RW): wave (wr, wc) owns WT = 16/RW
+// weight tiles (16 rows each) x CW route tiles, so its accumulators are
+// WT*CW MFMA tiles (the per-K-block scale FMAs need them in VGPRs, which
+// bounds the tile).  Weights are the MFMA A operand and stream from HBM
+// straight into a WS-slot register ring, WS-1 K-blocks ahead.  Routed
+// activations are the B operand: each K-block of the route tile is gathered
+// into registers AS+1 steps ahead (AS staging sets), then written to one of
+// two LDS buffers in the fragment layout and read by the RW row groups.
+// Every load goes to registers, so all waits are the compiler's own in-order
+// vmcnt waits; one barrier per K-block.
+//
+// A CU can only issue about one 1 KB vector load per 16 cycles, and a wave
+// issues in order: if a step's loads and LDS stores were issued up front,
+// every wave would sit in the load queue before its first MFMA and the data
+// movement would serialise with the math.  Instead each step issues its
+// side work (next weight tiles; activation stores and gathers) between
+// thirds of its MFMA work.
 #include "common.h"
 #include "gemm_util.h"
 #include "launch.h"
@@ -26,7 +34,7 @@
 namespace moe {
 namespace {
 
-constexpr int TW = 8;  // waves per workgroup (4 weight-row groups x 2 route halves)
+constexpr int TW = 8;  // waves per workgroup
 constexpr int TNT = TW * 64;
 
 template <int CT, int RW>
@@ -42,13 +50,14 @@ struct TileGeom {
 };
 
 // LDS layout of the activation stages: s_act[route tile c][buffer][2 KB]
-// fragment tiles, s_scl[buffer][BM] scales.  In a fragment tile, chunk
-// (route i, lane-group g, half h) sits at h*1024 + (g*16 + (i ^ 4g))*16:
-// lane l reads route l%16, group l/16, so each half is a permutation of the
-// 64 16-byte slots (conflict-free reads), and one lane offset serves both
+// fragment tiles, s_scl[buffer][BM] scales.  A fragment tile has the MFMA
+// operand's split-half layout (chunk (route i, lane-group g, half h) at
+// h*1024 + g*256 + i*16), so lane l reads bytes l*16.. of each half: the
+// reads are lane-contiguous (no bank conflicts on gfx950, where a permuted
+// 16-lane read costs half again as long), and one lane offset serves both
 // halves and every (tile, buffer) through the instruction's immediate offset
 // (c*4096 + buffer*2048 + h*1024 < 64 KB for CT <= 16).
-__device__ __forceinline__ int frag_slot(int i, int g, int h) { return h * 1024 + (g * 16 + (i ^ (g << 2))) * 16; }
+__device__ __forceinline__ int frag_slot(int i, int g, int h) { return h * 1024 + g * 256 + i * 16; }
 
 __device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
   const uint4 lo = *reinterpret_cast<const uint4*>(p);
@@ -57,39 +66,54 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
 }
 
 // Registers holding one K-block of the route tile on its way to LDS: this
-// thread's ACH 16-byte chunks (chunk x = tid + i*TNT: route x/8, K chunk x%8)
-// and, for tid < BM, route tid's activation scale.
+// thread's ACH 16-byte chunks and, for tid < BM, route tid's activation
+// scale.  Chunk x = tid + i*TNT is route 8*(x/64) + x%8, K chunk (x/8)%8: a
+// wave instruction still covers 8 whole 128-byte rows (full cache lines),
+// and its 8-lane groups store 8 routes' same chunk, 128 contiguous LDS bytes
+// (one route's 8 chunks would all fall in one bank group).  Row r's K-block starts at
+// abase + s_rowoff[r] + kofs, its scale at sbase[s_soff[r] + sofs]; padding
+// routes repeat route 0 (a real row).
+__device__ __forceinline__ int chunk_route(int x) { return ((x >> 6) << 3) | (x & 7); }
+__device__ __forceinline__ int chunk_k(int x) { return (x >> 3) & 7; }
+
 template <int CT, int RW>
 struct ActStage {
   using G = TileGeom<CT, RW>;
   uint4 v[G::ACH];
   float sc;
 
-  // row r's K-block starts at abase + s_rowoff[r] + kofs; its scale at
-  // sbase + s_soff[r] + sofs.  Padding routes repeat route 0 (a real row).
-  __device__ __forceinline__ void load(const uint8_t* __restrict__ abase, const long long* s_rowoff, size_t kofs,
-                                       const float* __restrict__ sbase, const int* s_soff, size_t sofs, int tid) {
-#pragma unroll
-    for (int i = 0; i < G::ACH; ++i) {
-      const int x = tid + i * TNT;
-      v[i] = (G::NCH % TNT == 0 || x < G::NCH)
-                 ? *reinterpret_cast<const uint4*>(abase + s_rowoff[x >> 3] + kofs + (x & 7) * 16)
-                 : make_uint4(0, 0, 0, 0);
-    }
+  __device__ __forceinline__ void load_chunk(int i, const uint8_t* __restrict__ abase, const long long* s_rowoff,
+                                             size_t kofs, int tid) {
+    const int x = tid + i * TNT;
+    v[i] = (G::NCH % TNT == 0 || x < G::NCH)
+               ? *reinterpret_cast<const uint4*>(abase + s_rowoff[chunk_route(x)] + kofs + chunk_k(x) * 16)
+               : make_uint4(0, 0, 0, 0);
+  }
+  __device__ __forceinline__ void load_scale(const float* __restrict__ sbase, const int* s_soff, size_t sofs,
+                                             int tid) {
     if (tid < G::BM) sc = sbase[s_soff[tid] + sofs];
   }
-
   // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM].
+  __device__ __forceinline__ void store_chunk(int i, uint8_t* s_act, int b, int tid) const {
+    const int x = tid + i * TNT;
+    if (G::NCH % TNT == 0 || x < G::NCH) {
+      const int r = chunk_route(x), q = chunk_k(x);
+      *reinterpret_cast<uint4*>(s_act + ((r >> 4) * 2 + b) * TILE_BYTES + frag_slot(r & 15, q >> 1, q & 1)) = v[i];
+    }
+  }
+  __device__ __forceinline__ void store_scale(float* s_scl, int b, int tid) const {
+    if (tid < G::BM) s_scl[b * G::BM + tid] = sc;
+  }
+  __device__ __forceinline__ void load(const uint8_t* abase, const long long* s_rowoff, size_t kofs,
+                                       const float* sbase, const int* s_soff, size_t sofs, int tid) {
+#pragma unroll
+    for (int i = 0; i < G::ACH; ++i) load_chunk(i, abase, s_rowoff, kofs, tid);
+    load_scale(sbase, s_soff, sofs, tid);
+  }
   __device__ __forceinline__ void store(uint8_t* s_act, float* s_scl, int b, int tid) const {
 #pragma unroll
-    for (int i = 0; i < G::ACH; ++i) {
-      const int x = tid + i * TNT;
-      if (G::NCH % TNT == 0 || x < G::NCH) {
-        const int r = x >> 3, q = x & 7;
-        *reinterpret_cast<uint4*>(s_act + ((r >> 4) * 2 + b) * TILE_BYTES + frag_slot(r & 15, q >> 1, q & 1)) = v[i];
-      }
-    }
-    if (tid < G::BM) s_scl[b * G::BM + tid] = sc;
+    for (int i = 0; i < G::ACH; ++i) store_chunk(i, s_act, b, tid);
+    store_scale(s_scl, b, tid);
   }
 };
 
@@ -97,35 +121,50 @@ struct ActStage {
 // Written as one statement so no VMEM wait is attached to it.
 __device__ __forceinline__ void step_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// One K-block of a wave's tile: acc[t][cc] += (W_t x B_cc) * (a_scale[cc] *
-// w_scale(t)) for its WT weight tiles (wf) and CW route tiles, B fragments
-// at af + cc*4096 and route scales at as_[cc*16] in LDS.  Software-pipelined
-// by one route tile: the scale FMAs of route tile cc-1 (whose MFMA results
-// are ready by then) run in the shadow of route tile cc's MFMAs instead of
-// stalling on them.  All CW route tiles are computed; padding routes hold a
-// copy of route 0 and their columns are never stored.
-template <int WT, int CW, typename WS>
-__device__ __forceinline__ void mma_step(v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af, const float* as_,
-                                         WS ws) {
-  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
-  float a[2];
-  v4f p[2][WT];
+// Route tiles C0..C1-1 of one K-block of a wave's tile: acc[t][cc] +=
+// (W_t x B_cc) * (a_scale[cc] * w_scale(t)) for its WT weight tiles (wf), B
+// fragments at af + cc*4096 and route scales at as_[cc*16] in LDS.
+// Software-pipelined: the B fragment of route tile cc+1 is read from LDS
+// while route tile cc's MFMAs run, and the scale FMAs of an earlier route
+// tile (whose MFMA results are ready by then) fill the MFMA shadow.  All route tiles are computed
+// (padding routes hold a copy of route 0 and their columns are never stored);
+// an empty range does nothing.
+template <int WT, int CW, int C0, int C1, typename WS>
+__device__ __forceinline__ void mma_part(v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af,
+                                         const float* as_, WS ws) {
+  static_assert(0 <= C0 && C0 <= C1 && C1 <= CW, "route tile range");
+  // FMAs of route tile cc run after the MFMAs of route tile cc+D: with WT
+  // MFMAs per route tile that puts >= 4 MFMAs between a result and its first
+  // VALU reader (measured on gfx950: MFMA + 4 dependent FMAs reaches ~79% of
+  // the MFMA rate at distance 4, ~66% at distance 1).
+  constexpr int D = (WT >= 4) ? 1 : 2;
+  constexpr int NB = D + 1;
+  if constexpr (C1 > C0) {
+    const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+    float a[NB];
+    v8i b[2];
+    v4f p[NB][WT];
+    b[C0 & 1] = lds_frag(af + C0 * 2 * TILE_BYTES);
 #pragma unroll
-  for (int cc = 0; cc < CW; ++cc) {
-    const int cur = cc & 1;
-    __asm__ volatile("" ::: "memory");  // no speculative hoisting of later tiles' LDS reads
-    const v8i b = lds_frag(af + cc * 2 * TILE_BYTES);
-    a[cur] = as_[cc * 16];
+    for (int cc = C0; cc < C1 + D; ++cc) {
+      if (cc < C1) {
+        // next route tile's fragment, read while this one's MFMAs run
+        if (cc + 1 < C1) b[(cc + 1) & 1] = lds_frag(af + (cc + 1) * 2 * TILE_BYTES);
+        a[cc % NB] = as_[cc * 16];
 #pragma unroll
-    for (int t = 0; t < WT; ++t) p[cur][t] = mfma_16x16x128_fp8(wf[t], b, zero4);
-    if (cc > 0) {
+        for (int t = 0; t < WT; ++t) p[cc % NB][t] = mfma_16x16x128_fp8(wf[t], b[cc & 1], zero4);
+      }
+      const int cf = cc - D;  // route tile whose scale FMAs run now
+      if (cf >= C0) {
 #pragma unroll
-      for (int t = 0; t < WT; ++t) acc[t][cc - 1] += p[cur ^ 1][t] * (a[cur ^ 1] * ws(t));
+        for (int t = 0; t < WT; ++t) {
+          acc[t][cf] += p[cf % NB][t] * (a[cf % NB] * ws(t));
+          __asm__ volatile("" : "+v"(acc[t][cf]));  // pin the FMAs here (no sinking past later steps)
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // one route tile per pipeline stage
     }
-    __builtin_amdgcn_sched_barrier(0);  // one route tile per pipeline stage
   }
-#pragma unroll
-  for (int t = 0; t < WT; ++t) acc[t][CW - 1] += p[(CW - 1) & 1][t] * (a[(CW - 1) & 1] * ws(t));
 }
 
 // ---------------------------------------------------------------------------
@@ -134,7 +173,7 @@ __device__ __forceinline__ void mma_step(v4f (&acc)[WT][CW], const v8i (&wf)[WT]
 // wr*WT .. wr*WT+WT-1 (gate/up pairs j = wr*WT/2 ..) x route tiles
 // wc*CW .. wc*CW+CW-1.
 // ---------------------------------------------------------------------------
-template <int CT, int RW>
+template <int CT, int RW, int WS, int AS>
 __global__ void __launch_bounds__(TNT)
 stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
                    const uint8_t* __restrict__ w13p, const float* __restrict__ w13s,
@@ -143,7 +182,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
                    int e_local) {
   using G = TileGeom<CT, RW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2;
-  static_assert(HB % 4 == 0, "four-step unroll");
+  static_assert(HB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
   __shared__ float s_scl[2 * BM];
   __shared__ long long s_rowoff[BM];
@@ -171,48 +210,55 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     }
     __syncthreads();
 
-    const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
-    const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
-    const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
     // This lane's fragment / scale addresses in LDS for route tile wc*CW.
     const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
     const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
-    v8i wf[4][WT];
-    auto wload = [&](int sl, int kb) {
-#pragma unroll
-      for (int t = 0; t < WT; ++t) wf[sl][t] = load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane);
-    };
+    const bool active = G::CG == 1 || wc * CW * 16 < rows;  // route groups past the tile's routes skip the MFMAs
+    const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
+    const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
+    const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
+    v8i wf[WS][WT];
+    auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane); };
     v4f acc[WT][CW];
 #pragma unroll
     for (int t = 0; t < WT; ++t)
 #pragma unroll
       for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
 
-    // Pipeline: weights two K-blocks ahead (4-slot register ring), activations
-    // gathered three ahead into two staging sets and stored to LDS one ahead.
-    ActStage<CT, RW> st[2];
-    wload(0, 0);
-    wload(1, 1);
-    st[0].load(hidden, s_rowoff, 0, hscale, s_soff, 0, tid);
-    st[1].load(hidden, s_rowoff, BLK, hscale, s_soff, (size_t)T, tid);
+    // Prologue: weights of K-blocks 0..WS-2, activations of 0..AS-1 gathered,
+    // K-block 0 in LDS buffer 0 and K-block AS gathered into set 0.
+    ActStage<CT, RW> st[AS];
+#pragma unroll
+    for (int w0 = 0; w0 < WS - 1; ++w0)
+#pragma unroll
+      for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
+#pragma unroll
+    for (int a0 = 0; a0 < AS; ++a0) st[a0].load(hidden, s_rowoff, (size_t)a0 * BLK, hscale, s_soff, (size_t)a0 * T, tid);
     st[0].store(s_act, s_scl, 0, tid);
-    st[0].load(hidden, s_rowoff, 2 * BLK, hscale, s_soff, 2 * (size_t)T, tid);
+    st[0].load(hidden, s_rowoff, (size_t)AS * BLK, hscale, s_soff, (size_t)AS * T, tid);
 
 #pragma unroll 1
     for (int kb0 = 0; kb0 < HB; kb0 += 4) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int kb = kb0 + s;
-        step_barrier();  // stage kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
-        wload((s + 2) & 3, min(kb + 2, HB - 1));
-        st[(s + 1) & 1].store(s_act, s_scl, (s + 1) & 1, tid);  // stage kb+1 (past the end: dead copies)
-        const int ka = min(kb + 3, HB - 1);
-        st[(s + 1) & 1].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
-        __builtin_amdgcn_sched_barrier(0);
+        step_barrier();  // K-block kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
         const float wsg = wsg_p[kb], wsu = wsu_p[kb];
-        if (wc * CW * 16 < rows)  // route groups past the tile's routes skip the MFMAs
-          mma_step<WT, CW>(acc, wf[s], afrag + (s & 1) * TILE_BYTES, ascl + (s & 1) * BM,
-                           [&](int t) { return (t & 1) ? wsu : wsg; });
+        const int kw = min(kb + WS - 1, HB - 1);  // past the end: dead re-reads of the last block
+        const int ka = min(kb + AS + 1, HB - 1);
+        auto ws = [&](int t) { return (t & 1) ? wsu : wsg; };
+        const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
+        const float* as_ = ascl + (s & 1) * BM;
+        // Side work between thirds of the MFMA work: the next weights, then
+        // K-block kb+1 from staging set (s+1)%AS into LDS buffer (kb+1)&1 and
+        // K-block kb+AS+1 gathered into that set.
+        if (active) mma_part<WT, CW, 0, CW / 3>(acc, wf[s % WS], af, as_, ws);
+#pragma unroll
+        for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
+        if (active) mma_part<WT, CW, CW / 3, 2 * CW / 3>(acc, wf[s % WS], af, as_, ws);
+        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid);
+        st[(s + 1) % AS].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
+        if (active) mma_part<WT, CW, 2 * CW / 3, CW>(acc, wf[s % WS], af, as_, ws);
       }
     }
 
@@ -268,7 +314,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 // 2hp+1, 16 row tiles) x routes mt*BM...  Wave (wr, wc) owns row tiles
 // wr*WT .. wr*WT+WT-1 x route tiles wc*CW ...  Y[r, h] = O[r, h] * weight[r].
 // ---------------------------------------------------------------------------
-template <int CT, int RW>
+template <int CT, int RW, int WS, int AS>
 __global__ void __launch_bounds__(TNT)
 stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
                    const float* __restrict__ w2s, const int32_t* __restrict__ counts,
@@ -276,7 +322,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
                    float* __restrict__ Y, int e_local) {
   using G = TileGeom<CT, RW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2;
-  static_assert(IB % 4 == 0, "four-step unroll");
+  static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
   __shared__ float s_scl[2 * BM];
   __shared__ long long s_rowoff[BM];
@@ -303,31 +349,30 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     }
     __syncthreads();
 
+    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
+    const bool active = G::CG == 1 || wc * CW * 16 < rows;
     const int g0 = wr * WT;  // first of this wave's 16 row tiles
     const int hb = 2 * hp + (g0 >> 3), t0 = g0 & 7;
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
     const float* ws_p = w2s + (size_t)(e * HB + hb) * IB;
-    // This lane's fragment / scale addresses in LDS for route tile wc*CW.
-    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
-    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
-    v8i wf[4][WT];
-    auto wload = [&](int sl, int kb) {
-#pragma unroll
-      for (int t = 0; t < WT; ++t) wf[sl][t] = load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane);
-    };
+    v8i wf[WS][WT];
+    auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane); };
     v4f acc[WT][CW];
 #pragma unroll
     for (int t = 0; t < WT; ++t)
 #pragma unroll
       for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
 
-    ActStage<CT, RW> st[2];
-    wload(0, 0);
-    wload(1, 1);
-    st[0].load(Cq, s_rowoff, 0, Cs, s_soff, 0, tid);
-    st[1].load(Cq, s_rowoff, BLK, Cs, s_soff, 1, tid);
+    ActStage<CT, RW> st[AS];
+#pragma unroll
+    for (int w0 = 0; w0 < WS - 1; ++w0)
+#pragma unroll
+      for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
+#pragma unroll
+    for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq, s_rowoff, (size_t)a0 * BLK, Cs, s_soff, (size_t)a0, tid);
     st[0].store(s_act, s_scl, 0, tid);
-    st[0].load(Cq, s_rowoff, 2 * BLK, Cs, s_soff, 2, tid);
+    st[0].load(Cq, s_rowoff, (size_t)AS * BLK, Cs, s_soff, (size_t)AS, tid);
 
 #pragma unroll 1
     for (int kb0 = 0; kb0 < IB; kb0 += 4) {
@@ -335,14 +380,19 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       for (int s = 0; s < 4; ++s) {
         const int kb = kb0 + s;
         step_barrier();
-        wload((s + 2) & 3, min(kb + 2, IB - 1));
-        st[(s + 1) & 1].store(s_act, s_scl, (s + 1) & 1, tid);
-        const int ka = min(kb + 3, IB - 1);
-        st[(s + 1) & 1].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
-        __builtin_amdgcn_sched_barrier(0);
-        const float ws = ws_p[kb];
-        if (wc * CW * 16 < rows)
-          mma_step<WT, CW>(acc, wf[s], afrag + (s & 1) * TILE_BYTES, ascl + (s & 1) * BM, [&](int) { return ws; });
+        const float wsv = ws_p[kb];
+        const int kw = min(kb + WS - 1, IB - 1);
+        const int ka = min(kb + AS + 1, IB - 1);
+        auto ws = [&](int) { return wsv; };
+        const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
+        const float* as_ = ascl + (s & 1) * BM;
+        if (active) mma_part<WT, CW, 0, CW / 3>(acc, wf[s % WS], af, as_, ws);
+#pragma unroll
+        for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
+        if (active) mma_part<WT, CW, CW / 3, 2 * CW / 3>(acc, wf[s % WS], af, as_, ws);
+        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid);
+        st[(s + 1) % AS].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
+        if (active) mma_part<WT, CW, 2 * CW / 3, CW>(acc, wf[s % WS], af, as_, ws);
       }
     }
 
@@ -371,24 +421,24 @@ TileShape tile_shape(int T) {
   return expected <= 64 ? TILE_64x256 : (expected <= 128 ? TILE_128x256 : TILE_192x256);
 }
 
-template <int CT, int RW>
+template <int CT, int RW, int WS, int AS>
 hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
                            const int32_t* counts, const int32_t* offsets, const int32_t* route_token, uint8_t* Cq,
                            float* Cs, int T, int e_local, int max_routes, hipStream_t stream) {
   constexpr int BM = TileGeom<CT, RW>::BM;
-  auto k = stage1_tile_kernel<CT, RW>;
+  auto k = stage1_tile_kernel<CT, RW, WS, AS>;
   const long long bound = ((long long)e_local + max_routes / BM + 1) * IB;
   const int grid = persistent_grid(bound, resident_blocks(k, TNT));
   k<<<grid, TNT, 0, stream>>>(hidden, hs, w13p, w13s, counts, offsets, route_token, Cq, Cs, T, e_local);
   return hipGetLastError();
 }
 
-template <int CT, int RW>
+template <int CT, int RW, int WS, int AS>
 hipError_t run_stage2_tile(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2s,
                            const int32_t* counts, const int32_t* offsets, const float* rw, float* Y, int e_local,
                            int max_routes, hipStream_t stream) {
   constexpr int BM = TileGeom<CT, RW>::BM;
-  auto k = stage2_tile_kernel<CT, RW>;
+  auto k = stage2_tile_kernel<CT, RW, WS, AS>;
   const long long bound = ((long long)e_local + max_routes / BM + 1) * (HB / 2);
   const int grid = persistent_grid(bound, resident_blocks(k, TNT));
   k<<<grid, TNT, 0, stream>>>(Cq, Cs, w2p, w2s, counts, offsets, rw, Y, e_local);
@@ -403,14 +453,14 @@ hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const
                          hipStream_t stream) {
   switch (tile_shape(T)) {
     case TILE_64x256:
-      return run_stage1_tile<4, 4>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
-                                   e_local, max_routes, stream);
+      return run_stage1_tile<4, 4, 4, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                         T, e_local, max_routes, stream);
     case TILE_128x256:
-      return run_stage1_tile<8, 4>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
-                                   e_local, max_routes, stream);
+      return run_stage1_tile<8, 8, 2, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                         T, e_local, max_routes, stream);
     default:
-      return run_stage1_tile<12, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
-                                    e_local, max_routes, stream);
+      return run_stage1_tile<12, 8, 2, 1>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
+                                          Cs, T, e_local, max_routes, stream);
   }
 }
 
@@ -419,14 +469,14 @@ hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p,
                          int e_local, int max_routes, hipStream_t stream) {
   switch (tile_shape(T)) {
     case TILE_64x256:
-      return run_stage2_tile<4, 4>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
-                                   stream);
+      return run_stage2_tile<4, 4, 4, 2>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                         max_routes, stream);
     case TILE_128x256:
-      return run_stage2_tile<8, 4>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
-                                   stream);
+      return run_stage2_tile<8, 8, 2, 2>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                         max_routes, stream);
     default:
-      return run_stage2_tile<12, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
-                                    stream);
+      return run_stage2_tile<12, 8, 2, 1>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                          max_routes, stream);
   }
 }
 
