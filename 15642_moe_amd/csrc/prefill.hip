@@ -24,9 +24,10 @@
 // A CU can only issue about one 1 KB vector load per 16 cycles, and a wave
 // issues in order: if a step's loads and LDS stores were issued up front,
 // every wave would sit in the load queue before its first MFMA and the data
-// movement would serialise with the math.  Instead each step issues its
-// side work (next weight tiles; activation stores and gathers) between
-// thirds of its MFMA work.
+// movement would serialise with the math.  A step therefore issues the next
+// weight tiles first, then its MFMAs, and only then stores the activation
+// K-block gathered one step earlier into LDS and starts the next gather:
+// each wait for a gather is covered by a whole step of MFMAs.
 #include "common.h"
 #include "gemm_util.h"
 #include "launch.h"
@@ -35,6 +36,9 @@ namespace moe {
 namespace {
 
 constexpr int TW = 8;  // waves per workgroup
+#ifndef LDS_AHEAD
+#define LDS_AHEAD 2
+#endif
 constexpr int TNT = TW * 64;
 
 template <int CT, int RW>
@@ -50,7 +54,7 @@ struct TileGeom {
 };
 
 // LDS layout of the activation stages: s_act[route tile c][buffer][2 KB]
-// fragment tiles, s_scl[buffer][BM] scales.  A fragment tile has the MFMA
+// fragment tiles, s_scl[buffer][BM] scale pairs.  A fragment tile has the MFMA
 // operand's split-half layout (chunk (route i, lane-group g, half h) at
 // h*1024 + g*256 + i*16), so lane l reads bytes l*16.. of each half: the
 // reads are lane-contiguous (no bank conflicts on gfx950, where a permuted
@@ -93,7 +97,7 @@ struct ActStage {
                                              int tid) {
     if (tid < G::BM) sc = sbase[s_soff[tid] + sofs];
   }
-  // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM].
+  // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM] (scale pairs).
   __device__ __forceinline__ void store_chunk(int i, uint8_t* s_act, int b, int tid) const {
     const int x = tid + i * TNT;
     if (G::NCH % TNT == 0 || x < G::NCH) {
@@ -101,8 +105,10 @@ struct ActStage {
       *reinterpret_cast<uint4*>(s_act + ((r >> 4) * 2 + b) * TILE_BYTES + frag_slot(r & 15, q >> 1, q & 1)) = v[i];
     }
   }
-  __device__ __forceinline__ void store_scale(float* s_scl, int b, int tid) const {
-    if (tid < G::BM) s_scl[b * G::BM + tid] = sc;
+  // Route tid's activation scale times the K-block's two weight-block scales,
+  // as one float2, so the MFMA loop needs no multiply per route tile.
+  __device__ __forceinline__ void store_scale(float2* s_scl, int b, int tid, float w0, float w1) const {
+    if (tid < G::BM) s_scl[b * G::BM + tid] = make_float2(sc * w0, sc * w1);
   }
   __device__ __forceinline__ void load(const uint8_t* abase, const long long* s_rowoff, size_t kofs,
                                        const float* sbase, const int* s_soff, size_t sofs, int tid) {
@@ -110,10 +116,10 @@ struct ActStage {
     for (int i = 0; i < G::ACH; ++i) load_chunk(i, abase, s_rowoff, kofs, tid);
     load_scale(sbase, s_soff, sofs, tid);
   }
-  __device__ __forceinline__ void store(uint8_t* s_act, float* s_scl, int b, int tid) const {
+  __device__ __forceinline__ void store(uint8_t* s_act, float2* s_scl, int b, int tid, float w0, float w1) const {
 #pragma unroll
     for (int i = 0; i < G::ACH; ++i) store_chunk(i, s_act, b, tid);
-    store_scale(s_scl, b, tid);
+    store_scale(s_scl, b, tid, w0, w1);
   }
 };
 
@@ -121,51 +127,73 @@ struct ActStage {
 // Written as one statement so no VMEM wait is attached to it.
 __device__ __forceinline__ void step_barrier() { __asm__ volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Route tiles C0..C1-1 of one K-block of a wave's tile: acc[t][cc] +=
-// (W_t x B_cc) * (a_scale[cc] * w_scale(t)) for its WT weight tiles (wf), B
-// fragments at af + cc*4096 and route scales at as_[cc*16] in LDS.
-// Software-pipelined: the B fragment of route tile cc+1 is read from LDS
-// while route tile cc's MFMAs run, and the scale FMAs of an earlier route
-// tile (whose MFMA results are ready by then) fill the MFMA shadow.  All route tiles are computed
-// (padding routes hold a copy of route 0 and their columns are never stored);
-// an empty range does nothing.
-template <int WT, int CW, int C0, int C1, typename WS>
-__device__ __forceinline__ void mma_part(v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af,
-                                         const float* as_, WS ws) {
-  static_assert(0 <= C0 && C0 <= C1 && C1 <= CW, "route tile range");
-  // FMAs of route tile cc run after the MFMAs of route tile cc+D: with WT
-  // MFMAs per route tile that puts >= 4 MFMAs between a result and its first
-  // VALU reader (measured on gfx950: MFMA + 4 dependent FMAs reaches ~79% of
-  // the MFMA rate at distance 4, ~66% at distance 1).
-  constexpr int D = (WT >= 4) ? 1 : 2;
-  constexpr int NB = D + 1;
-  if constexpr (C1 > C0) {
+// The MFMA work of one wave over the K-blocks of an item: per K-block and
+// route tile cc, acc[t][cc] += (W_t x B_cc) * scale for its WT weight tiles
+// (wf), with B fragments at af + cc*4096 in LDS and the route's scale
+// products (activation scale x weight-block scale, formed once per K-block
+// by the staging threads) at asp[cc*32]: with NS == 2 a float2 whose .x
+// serves the even weight tiles and .y the odd ones (gate / up), with NS == 1
+// one float for every tile.
+//
+// One software pipeline runs across route tiles and K-blocks: the B
+// fragments are read from LDS LP route tiles ahead of their MFMAs, and the
+// scale FMAs of a route tile run D route tiles after its MFMAs (>= 4 MFMAs
+// between a result and its first VALU reader; measured on gfx950, MFMA + 4
+// dependent FMAs reaches ~79% of the MFMA rate at distance 4 and ~66% at
+// distance 1).  The last D route tiles of a K-block finish during the next
+// K-block, so the pipeline never drains inside an item.  All route tiles are
+// computed (padding routes hold a copy of route 0; their columns are never
+// stored).
+template <int WT, int CW, int NS>
+struct MmaPipe {
+  static constexpr int D = (WT >= 4) ? 1 : 2;
+  static constexpr int NB = (D == 1) ? 2 : 4;  // result ring; divides 4*CW so slots are compile-time
+  static constexpr int LP = LDS_AHEAD;
+  v4f p[NB][WT];
+  float2 a[NB];
+
+  // Scale FMAs of ring slot `slot` into route tile column cf.
+  __device__ __forceinline__ void finish(v4f (&acc)[WT][CW], int slot, int cf) {
+#pragma unroll
+    for (int t = 0; t < WT; ++t) {
+      acc[t][cf] += p[slot][t] * ((NS == 2 && (t & 1)) ? a[slot].y : a[slot].x);
+      __asm__ volatile("" : "+v"(acc[t][cf]));  // pin the FMAs here (no sinking past later steps)
+    }
+  }
+
+  // K-block number S (mod 4) of the 4-step unrolled loop (a constant after
+  // unrolling, so every ring index folds); `first`: the item's first K-block
+  // (no earlier route tiles to finish).
+  __device__ __forceinline__ void step(int S, v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af,
+                                       const float* asp, bool first) {
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
-    float a[NB];
-    v8i b[2];
-    v4f p[NB][WT];
-    b[C0 & 1] = lds_frag(af + C0 * 2 * TILE_BYTES);
+    v8i b[LP + 1];
 #pragma unroll
-    for (int cc = C0; cc < C1 + D; ++cc) {
-      if (cc < C1) {
-        // next route tile's fragment, read while this one's MFMAs run
-        if (cc + 1 < C1) b[(cc + 1) & 1] = lds_frag(af + (cc + 1) * 2 * TILE_BYTES);
-        a[cc % NB] = as_[cc * 16];
+    for (int c = 0; c < LP && c < CW; ++c) b[c % (LP + 1)] = lds_frag(af + c * 2 * TILE_BYTES);
 #pragma unroll
-        for (int t = 0; t < WT; ++t) p[cc % NB][t] = mfma_16x16x128_fp8(wf[t], b[cc & 1], zero4);
-      }
-      const int cf = cc - D;  // route tile whose scale FMAs run now
-      if (cf >= C0) {
+    for (int cc = 0; cc < CW; ++cc) {
+      const int g = S * CW + cc;  // route tile number within the 4-step unroll
+      if (cc + LP < CW) b[(cc + LP) % (LP + 1)] = lds_frag(af + (cc + LP) * 2 * TILE_BYTES);
+      if constexpr (NS == 2) a[g % NB] = *reinterpret_cast<const float2*>(asp + cc * 32);
+      else a[g % NB].x = asp[cc * 32];
 #pragma unroll
-        for (int t = 0; t < WT; ++t) {
-          acc[t][cf] += p[cf % NB][t] * (a[cf % NB] * ws(t));
-          __asm__ volatile("" : "+v"(acc[t][cf]));  // pin the FMAs here (no sinking past later steps)
-        }
+      for (int t = 0; t < WT; ++t) p[g % NB][t] = mfma_16x16x128_fp8(wf[t], b[cc % (LP + 1)], zero4);
+      const int gf = g - D + 4 * CW;  // route tile finished now (mod 4*CW)
+      if (cc >= D) {
+        finish(acc, gf % NB, cc - D);
+      } else if (!first) {
+        finish(acc, gf % NB, cc - D + CW);
       }
       __builtin_amdgcn_sched_barrier(0);  // one route tile per pipeline stage
     }
   }
-}
+
+  // After the item's last K-block (S == 3): finish its last D route tiles.
+  __device__ __forceinline__ void drain(v4f (&acc)[WT][CW]) {
+#pragma unroll
+    for (int cc = CW - D; cc < CW; ++cc) finish(acc, (3 * CW + cc) % NB, cc);
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Stage 1.  Item (e, nb, mt): W13 rows of I-block nb (gate tiles 2j, up tiles
@@ -181,10 +209,10 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
                    const int32_t* __restrict__ route_token, uint8_t* __restrict__ Cq, float* __restrict__ Cs, int T,
                    int e_local) {
   using G = TileGeom<CT, RW>;
-  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2;
+  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2, NSC = 2;
   static_assert(HB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
-  __shared__ float s_scl[2 * BM];
+  __shared__ float2 s_scl[2 * BM];
   __shared__ long long s_rowoff[BM];
   __shared__ int s_soff[BM];
   __shared__ float s_red[RW][BM];
@@ -212,7 +240,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 
     // This lane's fragment / scale addresses in LDS for route tile wc*CW.
     const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
-    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
+    const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15));
     const bool active = G::CG == 1 || wc * CW * 16 < rows;  // route groups past the tile's routes skip the MFMAs
     const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
     const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
@@ -224,6 +252,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     for (int t = 0; t < WT; ++t)
 #pragma unroll
       for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+    MmaPipe<WT, CW, NSC> pipe;
 
     // Prologue: weights of K-blocks 0..WS-2, activations of 0..AS-1 gathered,
     // K-block 0 in LDS buffer 0 and K-block AS gathered into set 0.
@@ -234,7 +263,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
       for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
     for (int a0 = 0; a0 < AS; ++a0) st[a0].load(hidden, s_rowoff, (size_t)a0 * BLK, hscale, s_soff, (size_t)a0 * T, tid);
-    st[0].store(s_act, s_scl, 0, tid);
+    st[0].store(s_act, s_scl, 0, tid, wsg_p[0], wsu_p[0]);
     st[0].load(hidden, s_rowoff, (size_t)AS * BLK, hscale, s_soff, (size_t)AS * T, tid);
 
 #pragma unroll 1
@@ -243,24 +272,24 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
       for (int s = 0; s < 4; ++s) {
         const int kb = kb0 + s;
         step_barrier();  // K-block kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
-        const float wsg = wsg_p[kb], wsu = wsu_p[kb];
         const int kw = min(kb + WS - 1, HB - 1);  // past the end: dead re-reads of the last block
         const int ka = min(kb + AS + 1, HB - 1);
-        auto ws = [&](int t) { return (t & 1) ? wsu : wsg; };
+        const int k1 = min(kb + 1, HB - 1);
         const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
-        const float* as_ = ascl + (s & 1) * BM;
+        const float* asp = ascl + (s & 1) * 2 * BM;
         // Side work between thirds of the MFMA work: the next weights, then
         // K-block kb+1 from staging set (s+1)%AS into LDS buffer (kb+1)&1 and
         // K-block kb+AS+1 gathered into that set.
-        if (active) mma_part<WT, CW, 0, CW / 3>(acc, wf[s % WS], af, as_, ws);
 #pragma unroll
         for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-        if (active) mma_part<WT, CW, CW / 3, 2 * CW / 3>(acc, wf[s % WS], af, as_, ws);
-        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid);
+        if (active) pipe.step(s, acc, wf[s % WS], af, asp, kb == 0);
+        // After the MFMAs: K-block kb+1 (gathered a step ago) into LDS, then
+        // the gather of K-block kb+AS+1 into the freed staging set.
+        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, wsg_p[k1], wsu_p[k1]);
         st[(s + 1) % AS].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
-        if (active) mma_part<WT, CW, 2 * CW / 3, CW>(acc, wf[s % WS], af, as_, ws);
       }
     }
+    if (active) pipe.drain(acc);
 
     // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
 #pragma unroll
@@ -321,10 +350,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
                    const int32_t* __restrict__ offsets, const float* __restrict__ route_weight,
                    float* __restrict__ Y, int e_local) {
   using G = TileGeom<CT, RW>;
-  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2;
+  constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2, NSC = 1;
   static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
-  __shared__ float s_scl[2 * BM];
+  __shared__ float2 s_scl[2 * BM];
   __shared__ long long s_rowoff[BM];
   __shared__ int s_soff[BM];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
@@ -350,12 +379,13 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     __syncthreads();
 
     const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
-    const float* ascl = s_scl + wc * CW * 16 + (lane & 15);
     const bool active = G::CG == 1 || wc * CW * 16 < rows;
     const int g0 = wr * WT;  // first of this wave's 16 row tiles
     const int hb = 2 * hp + (g0 >> 3), t0 = g0 & 7;
+    // scale pair component (g0 >> 3) is this wave's H block
+    const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15)) + (g0 >> 3);
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
-    const float* ws_p = w2s + (size_t)(e * HB + hb) * IB;
+    const float* ws0_p = w2s + (size_t)(e * HB + 2 * hp) * IB;  // H block 2hp; 2hp+1 follows at +IB
     v8i wf[WS][WT];
     auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane); };
     v4f acc[WT][CW];
@@ -363,6 +393,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     for (int t = 0; t < WT; ++t)
 #pragma unroll
       for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+    MmaPipe<WT, CW, NSC> pipe;
 
     ActStage<CT, RW> st[AS];
 #pragma unroll
@@ -371,7 +402,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
     for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq, s_rowoff, (size_t)a0 * BLK, Cs, s_soff, (size_t)a0, tid);
-    st[0].store(s_act, s_scl, 0, tid);
+    st[0].store(s_act, s_scl, 0, tid, ws0_p[0], ws0_p[IB]);
     st[0].load(Cq, s_rowoff, (size_t)AS * BLK, Cs, s_soff, (size_t)AS, tid);
 
 #pragma unroll 1
@@ -380,21 +411,19 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       for (int s = 0; s < 4; ++s) {
         const int kb = kb0 + s;
         step_barrier();
-        const float wsv = ws_p[kb];
         const int kw = min(kb + WS - 1, IB - 1);
         const int ka = min(kb + AS + 1, IB - 1);
-        auto ws = [&](int) { return wsv; };
+        const int k1 = min(kb + 1, IB - 1);
         const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
-        const float* as_ = ascl + (s & 1) * BM;
-        if (active) mma_part<WT, CW, 0, CW / 3>(acc, wf[s % WS], af, as_, ws);
+        const float* asp = ascl + (s & 1) * 2 * BM;
 #pragma unroll
         for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-        if (active) mma_part<WT, CW, CW / 3, 2 * CW / 3>(acc, wf[s % WS], af, as_, ws);
-        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid);
+        if (active) pipe.step(s, acc, wf[s % WS], af, asp, kb == 0);
+        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, ws0_p[k1], ws0_p[IB + k1]);
         st[(s + 1) % AS].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
-        if (active) mma_part<WT, CW, 2 * CW / 3, CW>(acc, wf[s % WS], af, as_, ws);
       }
     }
+    if (active) pipe.drain(acc);
 
 #pragma unroll
     for (int cc = 0; cc < CW; ++cc) {
