@@ -61,6 +61,9 @@ def main() -> int:
     ap.add_argument("--configs", default="1,2,3,4", help="benchmark configs to time (headline: 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run one plain 512 MiB device copy (the known-size reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes) and exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -73,6 +76,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
+    if args.calibrate_copy:
+        return _calibrate_copy(torch)
     inputs_mod = importlib.import_module("15642_moe_amd.inputs")
     ops = importlib.import_module("15642_moe_amd.ops")
     capi = importlib.import_module("15642_moe_amd.capi")
@@ -259,6 +264,20 @@ def main() -> int:
         "configs": results,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+def _calibrate_copy(torch) -> int:
+    """One device-to-device copy of exactly 512 MiB (read 512 MiB, write
+    512 MiB): profiled with --pmc FETCH_SIZE / WRITE_SIZE it gives the factor
+    from counter kilobytes to bytes moved."""
+    n = 512 << 20
+    src = torch.full((n,), 1, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copied {n} bytes")
     return 0
 
 
