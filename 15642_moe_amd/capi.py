@@ -12,7 +12,7 @@ import ctypes
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("lib15642_moe_fp8.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MOE_OK = 0
 MOE_ERR_INVALID_ARG = 1
@@ -20,8 +20,9 @@ MOE_ERR_HIP = 2
 MOE_ERR_WORKSPACE = 3
 
 # Workspace buffer ids (enum moe_ws_buffer).
-WS_TOPK_IDS, WS_TOPK_W, WS_COUNTS, WS_OFFSETS, WS_ROUTE_TOKEN, WS_ROUTE_WEIGHT, WS_TOKEN_ROUTE, WS_CQ, WS_CS, WS_Y = range(10)
-WS_NBUF = 10
+(WS_TOPK_IDS, WS_TOPK_W, WS_COUNTS, WS_OFFSETS, WS_ROUTE_TOKEN, WS_ROUTE_WEIGHT, WS_TOKEN_ROUTE, WS_CQ, WS_CS, WS_Y,
+ WS_QUEUE) = range(11)
+WS_NBUF = 11
 FORWARD_EVENTS = 6
 
 _c_int, _c_size, _c_float, _c_vp, _c_u64 = ctypes.c_int, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p, ctypes.c_uint64

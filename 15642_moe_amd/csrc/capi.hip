@@ -53,6 +53,7 @@ size_t layout(int T, int e_local, size_t* off) {
       R * moe::I,                  // CQ
       R * moe::IB * 4,             // CS
       R * moe::H * 4,              // Y
+      (size_t)moe::QUEUE_COUNTERS * 4,  // QUEUE
   };
   size_t acc = 0;
   for (int b = 0; b < MOE_WS_NBUF; ++b) {
@@ -90,7 +91,8 @@ int route_and_dispatch(const float* logits, const float* bias, float rsf, int of
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_OFFSETS]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_ROUTE_TOKEN]),
                                           reinterpret_cast<float*>(ws + off[MOE_WS_ROUTE_WEIGHT]),
-                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]), st),
+                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]),
+                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]), st),
                      "dispatch_kernel launch"));
   return MOE_OK;
 }
@@ -206,6 +208,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
   uint8_t* Cq = ws + off[MOE_WS_CQ];
   float* Cs = reinterpret_cast<float*>(ws + off[MOE_WS_CS]);
   float* Y = reinterpret_cast<float*>(ws + off[MOE_WS_Y]);
+  int32_t* queue = reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]);
   const int R = (int)max_routes(T, e_local);
 
   MOE_TRY(mark(0));
@@ -227,16 +230,16 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
                        "stage2_decode_kernel launch"));
   } else {
     MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,
-                                            route_token, route_weight, token_route, st),
+                                            route_token, route_weight, token_route, queue, st),
                        "dispatch_kernel launch"));
     MOE_TRY(mark(2));
     MOE_TRY(hip_status(moe::launch_stage1(static_cast<const uint8_t*>(hidden), hidden_scale,
                                           static_cast<const uint8_t*>(w13_packed), w13_scale, counts, offsets,
-                                          route_token, Cq, Cs, T, e_local, R, st),
+                                          route_token, Cq, Cs, T, e_local, R, queue, st),
                        "stage1_kernel launch"));
     MOE_TRY(mark(3));
     MOE_TRY(hip_status(moe::launch_stage2(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts, offsets,
-                                          route_weight, Y, T, e_local, R, st),
+                                          route_weight, Y, T, e_local, R, queue + moe::QUEUE_COUNTERS / 2, st),
                        "stage2_kernel launch"));
   }
   MOE_TRY(mark(4));

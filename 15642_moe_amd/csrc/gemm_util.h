@@ -22,19 +22,6 @@ __device__ __forceinline__ v8i load_tile_frag(const uint8_t* __restrict__ tile, 
   return make_v8i(lo, hi);
 }
 
-// Slot -> logical work index.  Workgroup p always runs on XCD p % 8; within
-// each round of G slots, XCD x receives a contiguous run of logical works, so
-// the route tiles and weight blocks that share data run on one XCD (and its
-// L2) at the same time.
-__device__ __forceinline__ int xcd_logical(int slot, int G, int n_work) {
-  const int round0 = slot - slot % G;
-  const int p = slot - round0;
-  const int n_rem = min(G, n_work - round0);
-  const int x = p & 7, q = p >> 3;
-  const int base = n_rem >> 3, extra = n_rem & 7;
-  return round0 + x * base + min(x, extra) + q;
-}
-
 // Per-workgroup table of route tiles per local expert: expert e owns route
 // tiles s_tp[e] .. s_tp[e+1]-1 of BM routes each.
 template <int BM>
@@ -56,18 +43,19 @@ __device__ __forceinline__ void load_tile_table(const int32_t* __restrict__ coun
 }
 
 // Logical work L -> (expert, weight block, route tile).  Works are ordered
-// expert-major, then route tile, then weight block: the weight blocks that
-// read one route tile's activations are neighbours, so they run on one XCD
-// in the same round and the tile is fetched into that XCD's L2 once (the
-// activations are re-read by every weight block, the weights only by the
-// expert's few route tiles).
+// expert-major, then weight block, then route tile: the route tiles that
+// read one weight block are neighbours, so a contiguous run of works on one
+// XCD fetches each weight K-block into that XCD's L2 once for all of them
+// (an expert's route tiles also re-read their activations once per weight
+// block, but a route tile's K-block is smaller than a weight block's).
 __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const int* s_tp, int& e, int& blk,
                                             int& mt) {
   e = 0;
   while (e + 1 < e_local && s_tp[e + 1] * nblk <= L) ++e;
+  const int nt = s_tp[e + 1] - s_tp[e];  // >= 1: L lies inside expert e's works
   const int local = L - s_tp[e] * nblk;
-  mt = local / nblk;
-  blk = local - mt * nblk;
+  blk = local / nt;
+  mt = local - blk * nt;
 }
 
 // ---------------------------------------------------------------------------

@@ -10,7 +10,7 @@ hipError_t launch_route(const float* logits, const float* bias, float rsf, int T
                         float* topk_w, hipStream_t stream);
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
-                           int32_t* token_route, hipStream_t stream);
+                           int32_t* token_route, int32_t* queue, hipStream_t stream);
 hipError_t launch_combine(const float* Y, const int32_t* token_route, int T, uint16_t* out,
                           hipStream_t stream);
 
@@ -19,15 +19,16 @@ hipError_t launch_pack_w2(const uint8_t* w2, uint8_t* packed, int e_local, bool 
 hipError_t launch_fill_normal_e4m3(uint8_t* out, size_t n, uint64_t seed, uint64_t stream_id,
                                    hipStream_t stream);
 
-// Grouped GEMMs.  `rows_hint` = maximum routes per expert the host expects
-// (it only selects the tile shape; any value is correct).
+// Prefill grouped GEMMs.  `max_routes` bounds the routes of the launch (it
+// sizes the persistent grid); `queue` = QUEUE_COUNTERS / 2 work-queue
+// counters, zero at launch (the dispatch kernel clears all QUEUE_COUNTERS).
 hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local,
-                         int max_routes, hipStream_t stream);
+                         int max_routes, int32_t* queue, hipStream_t stream);
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
-                         float* Y, int T, int e_local, int max_routes, hipStream_t stream);
+                         float* Y, int T, int e_local, int max_routes, int32_t* queue, hipStream_t stream);
 
 // Decode path (T <= DECODE_MAX_T): GEMM1 + SwiGLU with the local dispatch
 // fused in (fp32 output Cf), the FP8 requant, then GEMM2 over 64-row items.

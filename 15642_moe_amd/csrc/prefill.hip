@@ -32,29 +32,31 @@
 #include "gemm_util.h"
 #include "launch.h"
 
+#include <type_traits>
+
 namespace moe {
 namespace {
 
-constexpr int TW = 8;  // waves per workgroup
 #ifndef LDS_AHEAD
 #define LDS_AHEAD 2
 #endif
-constexpr int TNT = TW * 64;
 
-template <int CT, int RW>
+// CT route tiles per item, RW row groups, NW waves per workgroup.
+template <int CT, int RW, int NW>
 struct TileGeom {
+  static constexpr int NT = NW * 64;               // threads per workgroup
   static constexpr int BM = 16 * CT;               // routes per tile
   static constexpr int WT = 16 / RW;               // weight tiles per wave (16 per 256-row item)
-  static constexpr int CG = TW / RW;               // route groups
+  static constexpr int CG = NW / RW;               // route groups
   static constexpr int CW = CT / CG;               // route tiles per wave
   static constexpr int NCH = BM * 8;               // 16-byte chunks per K-block of the route tile
-  static constexpr int ACH = (NCH + TNT - 1) / TNT;
-  static_assert((RW == 4 || RW == 8) && CT % CG == 0 && CT <= 16, "tile shape");
-  static_assert(BM <= TNT, "one scale per thread");
+  static constexpr int ACH = (NCH + NT - 1) / NT;
+  static_assert((RW == 4 || RW == 8) && NW % RW == 0 && CT % CG == 0 && CT <= 16, "tile shape");
+  static_assert(BM <= NT, "one scale per thread");
 };
 
 // LDS layout of the activation stages: s_act[route tile c][buffer][2 KB]
-// fragment tiles, s_scl[buffer][BM] scale pairs.  A fragment tile has the MFMA
+// fragment tiles, s_scl[buffer][NT] scale pairs (the first BM used).  A fragment tile has the MFMA
 // operand's split-half layout (chunk (route i, lane-group g, half h) at
 // h*1024 + g*256 + i*16), so lane l reads bytes l*16.. of each half: the
 // reads are lane-contiguous (no bank conflicts on gfx950, where a permuted
@@ -71,44 +73,51 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
 
 // Registers holding one K-block of the route tile on its way to LDS: this
 // thread's ACH 16-byte chunks and, for tid < BM, route tid's activation
-// scale.  Chunk x = tid + i*TNT is route 8*(x/64) + x%8, K chunk (x/8)%8: a
+// scale.  Chunk x = tid + i*NT is route 8*(x/64) + x%8, K chunk (x/8)%8: a
 // wave instruction still covers 8 whole 128-byte rows (full cache lines),
 // and its 8-lane groups store 8 routes' same chunk, 128 contiguous LDS bytes
 // (one route's 8 chunks would all fall in one bank group).  Row r's K-block starts at
 // abase + s_rowoff[r] + kofs, its scale at sbase[s_soff[r] + sofs]; padding
-// routes repeat route 0 (a real row).
+// routes take route 0's offsets (a real row).
 __device__ __forceinline__ int chunk_route(int x) { return ((x >> 6) << 3) | (x & 7); }
 __device__ __forceinline__ int chunk_k(int x) { return (x >> 3) & 7; }
 
-template <int CT, int RW>
+template <int CT, int RW, int NW>
 struct ActStage {
-  using G = TileGeom<CT, RW>;
+  using G = TileGeom<CT, RW, NW>;
   uint4 v[G::ACH];
   float sc;
 
+  // Every load of the K loop is issued unconditionally (padding routes read
+  // route 0's row, threads past BM route 0's scale): with a load skipped on
+  // some path the compiler's vmcnt waits must assume the shorter count, and
+  // the first MFMA of a step would then also wait for the previous step's
+  // gathers.
   __device__ __forceinline__ void load_chunk(int i, const uint8_t* __restrict__ abase, const long long* s_rowoff,
                                              size_t kofs, int tid) {
-    const int x = tid + i * TNT;
-    v[i] = (G::NCH % TNT == 0 || x < G::NCH)
+    const int x = tid + i * G::NT;
+    v[i] = (G::NCH % G::NT == 0 || x < G::NCH)
                ? *reinterpret_cast<const uint4*>(abase + s_rowoff[chunk_route(x)] + kofs + chunk_k(x) * 16)
                : make_uint4(0, 0, 0, 0);
   }
   __device__ __forceinline__ void load_scale(const float* __restrict__ sbase, const int* s_soff, size_t sofs,
                                              int tid) {
-    if (tid < G::BM) sc = sbase[s_soff[tid] + sofs];
+    sc = sbase[s_soff[tid < G::BM ? tid : 0] + sofs];
   }
   // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM] (scale pairs).
   __device__ __forceinline__ void store_chunk(int i, uint8_t* s_act, int b, int tid) const {
-    const int x = tid + i * TNT;
-    if (G::NCH % TNT == 0 || x < G::NCH) {
+    const int x = tid + i * G::NT;
+    if (G::NCH % G::NT == 0 || x < G::NCH) {
       const int r = chunk_route(x), q = chunk_k(x);
       *reinterpret_cast<uint4*>(s_act + ((r >> 4) * 2 + b) * TILE_BYTES + frag_slot(r & 15, q >> 1, q & 1)) = v[i];
     }
   }
   // Route tid's activation scale times the K-block's two weight-block scales,
-  // as one float2, so the MFMA loop needs no multiply per route tile.
+  // as one float2, so the MFMA loop needs no multiply per route tile.  All
+  // threads store (slots past BM are never read; a uniform count of LDS
+  // operations keeps the compiler's lgkmcnt waits exact).
   __device__ __forceinline__ void store_scale(float2* s_scl, int b, int tid, float w0, float w1) const {
-    if (tid < G::BM) s_scl[b * G::BM + tid] = make_float2(sc * w0, sc * w1);
+    s_scl[b * G::NT + tid] = make_float2(sc * w0, sc * w1);
   }
   __device__ __forceinline__ void load(const uint8_t* abase, const long long* s_rowoff, size_t kofs,
                                        const float* sbase, const int* s_soff, size_t sofs, int tid) {
@@ -141,9 +150,9 @@ __device__ __forceinline__ void step_barrier() { __asm__ volatile("s_waitcnt lgk
 // between a result and its first VALU reader; measured on gfx950, MFMA + 4
 // dependent FMAs reaches ~79% of the MFMA rate at distance 4 and ~66% at
 // distance 1).  The last D route tiles of a K-block finish during the next
-// K-block, so the pipeline never drains inside an item.  All route tiles are
-// computed (padding routes hold a copy of route 0; their columns are never
-// stored).
+// K-block, so the pipeline never drains inside an item.  The pipeline runs
+// over the wave's first NC route tiles only (a compile-time count, see
+// with_tile_count): route tiles past the item's routes cost nothing.
 template <int WT, int CW, int NS>
 struct MmaPipe {
   static constexpr int D = (WT >= 4) ? 1 : 2;
@@ -163,37 +172,72 @@ struct MmaPipe {
 
   // K-block number S (mod 4) of the 4-step unrolled loop (a constant after
   // unrolling, so every ring index folds); `first`: the item's first K-block
-  // (no earlier route tiles to finish).
+  // (no earlier route tiles to finish).  NC: route tiles computed (<= CW).
+  template <int NC>
   __device__ __forceinline__ void step(int S, v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af,
                                        const float* asp, bool first) {
+    static_assert(NC <= CW && NC >= D, "tile count");
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v8i b[LP + 1];
 #pragma unroll
-    for (int c = 0; c < LP && c < CW; ++c) b[c % (LP + 1)] = lds_frag(af + c * 2 * TILE_BYTES);
+    for (int c = 0; c < LP && c < NC; ++c) b[c % (LP + 1)] = lds_frag(af + c * 2 * TILE_BYTES);
 #pragma unroll
-    for (int cc = 0; cc < CW; ++cc) {
-      const int g = S * CW + cc;  // route tile number within the 4-step unroll
-      if (cc + LP < CW) b[(cc + LP) % (LP + 1)] = lds_frag(af + (cc + LP) * 2 * TILE_BYTES);
+    for (int cc = 0; cc < NC; ++cc) {
+      const int g = S * NC + cc;  // route tile number within the 4-step unroll
+      if (cc + LP < NC) b[(cc + LP) % (LP + 1)] = lds_frag(af + (cc + LP) * 2 * TILE_BYTES);
       if constexpr (NS == 2) a[g % NB] = *reinterpret_cast<const float2*>(asp + cc * 32);
       else a[g % NB].x = asp[cc * 32];
 #pragma unroll
       for (int t = 0; t < WT; ++t) p[g % NB][t] = mfma_16x16x128_fp8(wf[t], b[cc % (LP + 1)], zero4);
-      const int gf = g - D + 4 * CW;  // route tile finished now (mod 4*CW)
+      const int gf = g - D + 4 * NC;  // route tile finished now (mod 4*NC)
       if (cc >= D) {
         finish(acc, gf % NB, cc - D);
-      } else if (!first) {
-        finish(acc, gf % NB, cc - D + CW);
+      } else if (!first && cc - D + NC >= 0) {
+        finish(acc, gf % NB, cc - D + NC);
       }
       __builtin_amdgcn_sched_barrier(0);  // one route tile per pipeline stage
     }
   }
 
   // After the item's last K-block (S == 3): finish its last D route tiles.
+  template <int NC>
   __device__ __forceinline__ void drain(v4f (&acc)[WT][CW]) {
 #pragma unroll
-    for (int cc = CW - D; cc < CW; ++cc) finish(acc, (3 * CW + cc) % NB, cc);
+    for (int cc = (NC > D ? NC - D : 0); cc < NC; ++cc) finish(acc, (3 * NC + cc) % NB, cc);
   }
 };
+
+// Granularity of the per-item route-tile count: pairs of route tiles for
+// the 2-weight-tile waves (their pipeline distance is 2 route tiles), single
+// route tiles otherwise.
+template <int CW>
+struct TileQ {
+  static constexpr int Q = (CW >= 8) ? 2 : 1;
+};
+
+// Dynamic item distribution.  The logical items (decode_work order) are cut
+// into nq equal contiguous segments; segment q belongs to the workgroups p
+// with p % nq == q, which for nq == 8 all run on XCD q (workgroup p runs on
+// XCD p % 8).  They take the segment's items in order from counter q, so the
+// items that share an expert's weight block or a route tile's activations
+// run on one XCD (one L2) at about the same time, and pulling items evens
+// out their unequal times inside the XCD.  Equal item counts per segment:
+// an item's time depends little on how many of its route tiles hold routes
+// (the weight stream and the per-step work are paid in full).
+
+// Runs f(std::integral_constant<int, NC>) for the wave's route-tile count
+// ncc (0..CW, wave-uniform) rounded up to a multiple of Q: each count has
+// its own straight-line K loop, so padding route tiles of partly filled
+// items cost no LDS reads, MFMAs or FMAs.
+template <int Q, int N, typename F>
+__device__ __forceinline__ void with_tile_count(int ncc, F&& f) {
+  if constexpr (N <= 0) {
+    f(std::integral_constant<int, 0>{});  // a route group past the item's routes: staging only
+  } else {
+    if (ncc > N - Q) f(std::integral_constant<int, N>{});
+    else with_tile_count<Q, N - Q>(ncc, f);
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Stage 1.  Item (e, nb, mt): W13 rows of I-block nb (gate tiles 2j, up tiles
@@ -201,37 +245,44 @@ struct MmaPipe {
 // wr*WT .. wr*WT+WT-1 (gate/up pairs j = wr*WT/2 ..) x route tiles
 // wc*CW .. wc*CW+CW-1.
 // ---------------------------------------------------------------------------
-template <int CT, int RW, int WS, int AS>
-__global__ void __launch_bounds__(TNT)
+template <int CT, int RW, int WS, int AS, int NW>
+__global__ void __launch_bounds__(NW * 64)
 stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
                    const uint8_t* __restrict__ w13p, const float* __restrict__ w13s,
                    const int32_t* __restrict__ counts, const int32_t* __restrict__ offsets,
                    const int32_t* __restrict__ route_token, uint8_t* __restrict__ Cq, float* __restrict__ Cs, int T,
-                   int e_local) {
-  using G = TileGeom<CT, RW>;
+                   int e_local, int32_t* __restrict__ queue) {
+  using G = TileGeom<CT, RW, NW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2, NSC = 2;
   static_assert(HB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
-  __shared__ float2 s_scl[2 * BM];
+  __shared__ float2 s_scl[2 * G::NT];
   __shared__ long long s_rowoff[BM];
   __shared__ int s_soff[BM];
   __shared__ float s_red[RW][BM];
-  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
+  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = w % RW, wc = (RW == TW) ? 0 : w / RW;
+  const int wr = w % RW, wc = (RW == NW) ? 0 : w / RW;
   load_tile_table<BM>(counts, offsets, e_local, s_tp, s_cnt, s_off);
-  const int n_work = s_tp[e_local] * IB;
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  for (int slot = blockIdx.x; slot < n_work; slot += gridDim.x) {
+  const int nq = min(XCDS, (int)gridDim.x), q = blockIdx.x % nq;
+  const int n_work = s_tp[e_local] * IB;
+  const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
+
+  for (;;) {
+    if (tid == 0) s_item = seg_lo + atomicAdd(&queue[q], 1);
+    __syncthreads();
+    const int L = __builtin_amdgcn_readfirstlane(s_item);
+    if (L >= seg_hi) break;
     int e, nb, mt;
-    decode_work(xcd_logical(slot, gridDim.x, n_work), IB, e_local, s_tp, e, nb, mt);
+    decode_work(L, IB, e_local, s_tp, e, nb, mt);
     const int m0 = mt * BM;
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
-    for (int r = tid; r < BM; r += TNT) {
+    for (int r = tid; r < BM; r += G::NT) {
       const int tok = route_token[rb + (r < rows ? r : 0)];
       s_rowoff[r] = (long long)tok * H;
       s_soff[r] = tok;
@@ -241,99 +292,106 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     // This lane's fragment / scale addresses in LDS for route tile wc*CW.
     const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
     const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15));
-    const bool active = G::CG == 1 || wc * CW * 16 < rows;  // route groups past the tile's routes skip the MFMAs
+    // Route tiles of this wave that hold routes (0 for route groups past the tile's routes).
+    const int ncc = __builtin_amdgcn_readfirstlane(min(CW, max(0, (rows - wc * CW * 16 + 15) >> 4)));
     const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
     const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
     const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
-    v8i wf[WS][WT];
-    auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane); };
-    v4f acc[WT][CW];
+    // One instantiation of the item body per route-tile count (prologue, K
+    // loop and epilogue), so no accumulator crosses between them.
+    with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
+      constexpr int NC = decltype(nct)::value;
+      v8i wf[WS][WT];
+      auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane); };
+      v4f acc[WT][CW];
 #pragma unroll
-    for (int t = 0; t < WT; ++t)
+      for (int t = 0; t < WT; ++t)
 #pragma unroll
-      for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
-    MmaPipe<WT, CW, NSC> pipe;
+        for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+      MmaPipe<WT, CW, NSC> pipe;
 
-    // Prologue: weights of K-blocks 0..WS-2, activations of 0..AS-1 gathered,
-    // K-block 0 in LDS buffer 0 and K-block AS gathered into set 0.
-    ActStage<CT, RW> st[AS];
+      // Prologue: weights of K-blocks 0..WS-2, activations of 0..AS-1 gathered,
+      // K-block 0 in LDS buffer 0 and K-block AS gathered into set 0.
+      ActStage<CT, RW, NW> st[AS];
 #pragma unroll
-    for (int w0 = 0; w0 < WS - 1; ++w0)
+      for (int w0 = 0; w0 < WS - 1; ++w0)
 #pragma unroll
-      for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
+        for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
-    for (int a0 = 0; a0 < AS; ++a0) st[a0].load(hidden, s_rowoff, (size_t)a0 * BLK, hscale, s_soff, (size_t)a0 * T, tid);
-    st[0].store(s_act, s_scl, 0, tid, wsg_p[0], wsu_p[0]);
-    st[0].load(hidden, s_rowoff, (size_t)AS * BLK, hscale, s_soff, (size_t)AS * T, tid);
+      for (int a0 = 0; a0 < AS; ++a0)
+        st[a0].load(hidden, s_rowoff, (size_t)a0 * BLK, hscale, s_soff, (size_t)a0 * T, tid);
+      st[0].store(s_act, s_scl, 0, tid, wsg_p[0], wsu_p[0]);
+      st[0].load(hidden, s_rowoff, (size_t)AS * BLK, hscale, s_soff, (size_t)AS * T, tid);
 
 #pragma unroll 1
-    for (int kb0 = 0; kb0 < HB; kb0 += 4) {
+      for (int kb0 = 0; kb0 < HB; kb0 += 4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int kb = kb0 + s;
-        step_barrier();  // K-block kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
-        const int kw = min(kb + WS - 1, HB - 1);  // past the end: dead re-reads of the last block
-        const int ka = min(kb + AS + 1, HB - 1);
-        const int k1 = min(kb + 1, HB - 1);
-        const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
-        const float* asp = ascl + (s & 1) * 2 * BM;
-        // Side work between thirds of the MFMA work: the next weights, then
-        // K-block kb+1 from staging set (s+1)%AS into LDS buffer (kb+1)&1 and
-        // K-block kb+AS+1 gathered into that set.
+        for (int s = 0; s < 4; ++s) {
+          const int kb = kb0 + s;
+          step_barrier();  // K-block kb is in LDS buffer kb&1; buffer (kb+1)&1 is free
+          const int kw = min(kb + WS - 1, HB - 1);  // past the end: dead re-reads of the last block
+          const int ka = min(kb + AS + 1, HB - 1);
+          const int k1 = min(kb + 1, HB - 1);
+          const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
+          const float* asp = ascl + (s & 1) * 2 * G::NT;
+          // The next weights, then the MFMAs, then K-block kb+1 (gathered a
+          // step ago) from staging set (s+1)%AS into LDS buffer (kb+1)&1 and
+          // the gather of K-block kb+AS+1 into the freed set.
 #pragma unroll
-        for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-        if (active) pipe.step(s, acc, wf[s % WS], af, asp, kb == 0);
-        // After the MFMAs: K-block kb+1 (gathered a step ago) into LDS, then
-        // the gather of K-block kb+AS+1 into the freed staging set.
-        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, wsg_p[k1], wsu_p[k1]);
-        st[(s + 1) % AS].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
+          for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
+          if constexpr (NC > 0) pipe.template step<NC>(s, acc, wf[s % WS], af, asp, kb == 0);
+          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, wsg_p[k1], wsu_p[k1]);
+          __builtin_amdgcn_sched_barrier(0);  // the set's registers are free only after its stores
+          st[(s + 1) % AS].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
+        }
       }
-    }
-    if (active) pipe.drain(acc);
+      if constexpr (NC > 0) pipe.template drain<NC>(acc);
 
-    // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
+      // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
 #pragma unroll
-    for (int jj = 0; jj < NP; ++jj)
+      for (int cc = 0; cc < NC; ++cc) {
 #pragma unroll
-      for (int cc = 0; cc < CW; ++cc)
+        for (int jj = 0; jj < NP; ++jj)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float g = acc[2 * jj][cc][v], u = acc[2 * jj + 1][cc][v];
-          acc[2 * jj][cc][v] = (u / (1.0f + __expf(-u))) * g;
-        }
-    // Per-route amax over this wave's I columns, then over the RW row groups.
-#pragma unroll
-    for (int cc = 0; cc < CW; ++cc) {
-      float m = 0.0f;
-#pragma unroll
-      for (int jj = 0; jj < NP; ++jj)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(acc[2 * jj][cc][v]));
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
-      if (lane < 16) s_red[wr][(wc * CW + cc) * 16 + lane] = m;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int cc = 0; cc < CW; ++cc) {
-      const int row = (wc * CW + cc) * 16 + (lane & 15);
-      if (row < rows) {
-        float am = s_red[0][row];
-#pragma unroll
-        for (int r2 = 1; r2 < RW; ++r2) am = fmaxf(am, s_red[r2][row]);
-        const float sc = fmaxf(am / E4M3_MAX, 1.0e-8f);
-        uint8_t* crow = Cq + (size_t)(rb + row) * I + nb * BLK + 4 * (lane >> 4);
-#pragma unroll
-        for (int jj = 0; jj < NP; ++jj) {
-          float q[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(acc[2 * jj][cc][v] / sc, -E4M3_MAX), E4M3_MAX);
-          const uint32_t packed = cvt2_e4m3(q[0], q[1]) | (cvt2_e4m3(q[2], q[3]) << 16);
-          *reinterpret_cast<uint32_t*>(crow + 16 * (wr * NP + jj)) = packed;
-        }
-        if (wr == 0 && lane < 16) Cs[(size_t)(rb + row) * IB + nb] = sc;
+          for (int v = 0; v < 4; ++v) {
+            const float g = acc[2 * jj][cc][v], u = acc[2 * jj + 1][cc][v];
+            acc[2 * jj][cc][v] = (u / (1.0f + __expf(-u))) * g;
+          }
       }
-    }
+      // Per-route amax over this wave's I columns, then over the RW row groups.
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        float m = 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < NP; ++jj)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) m = fmaxf(m, fabsf(acc[2 * jj][cc][v]));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (lane < 16) s_red[wr][(wc * CW + cc) * 16 + lane] = m;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const int row = (wc * CW + cc) * 16 + (lane & 15);
+        if (row < rows) {
+          float am = s_red[0][row];
+#pragma unroll
+          for (int r2 = 1; r2 < RW; ++r2) am = fmaxf(am, s_red[r2][row]);
+          const float sc = fmaxf(am / E4M3_MAX, 1.0e-8f);
+          uint8_t* crow = Cq + (size_t)(rb + row) * I + nb * BLK + 4 * (lane >> 4);
+#pragma unroll
+          for (int jj = 0; jj < NP; ++jj) {
+            float q[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(acc[2 * jj][cc][v] / sc, -E4M3_MAX), E4M3_MAX);
+            const uint32_t packed = cvt2_e4m3(q[0], q[1]) | (cvt2_e4m3(q[2], q[3]) << 16);
+            *reinterpret_cast<uint32_t*>(crow + 16 * (wr * NP + jj)) = packed;
+          }
+          if (wr == 0 && lane < 16) Cs[(size_t)(rb + row) * IB + nb] = sc;
+        }
+      }
+    });
     __syncthreads();
   }
 }
@@ -343,35 +401,42 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 // 2hp+1, 16 row tiles) x routes mt*BM...  Wave (wr, wc) owns row tiles
 // wr*WT .. wr*WT+WT-1 x route tiles wc*CW ...  Y[r, h] = O[r, h] * weight[r].
 // ---------------------------------------------------------------------------
-template <int CT, int RW, int WS, int AS>
-__global__ void __launch_bounds__(TNT)
+template <int CT, int RW, int WS, int AS, int NW>
+__global__ void __launch_bounds__(NW * 64)
 stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
                    const float* __restrict__ w2s, const int32_t* __restrict__ counts,
                    const int32_t* __restrict__ offsets, const float* __restrict__ route_weight,
-                   float* __restrict__ Y, int e_local) {
-  using G = TileGeom<CT, RW>;
+                   float* __restrict__ Y, int e_local, int32_t* __restrict__ queue) {
+  using G = TileGeom<CT, RW, NW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2, NSC = 1;
   static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
-  __shared__ float2 s_scl[2 * BM];
+  __shared__ float2 s_scl[2 * G::NT];
   __shared__ long long s_rowoff[BM];
   __shared__ int s_soff[BM];
-  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
+  __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wr = w % RW, wc = (RW == TW) ? 0 : w / RW;
+  const int wr = w % RW, wc = (RW == NW) ? 0 : w / RW;
   load_tile_table<BM>(counts, offsets, e_local, s_tp, s_cnt, s_off);
-  const int n_work = s_tp[e_local] * NHP;
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
 
-  for (int slot = blockIdx.x; slot < n_work; slot += gridDim.x) {
+  const int nq = min(XCDS, (int)gridDim.x), q = blockIdx.x % nq;
+  const int n_work = s_tp[e_local] * NHP;
+  const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
+
+  for (;;) {
+    if (tid == 0) s_item = seg_lo + atomicAdd(&queue[q], 1);
+    __syncthreads();
+    const int L = __builtin_amdgcn_readfirstlane(s_item);
+    if (L >= seg_hi) break;
     int e, hp, mt;
-    decode_work(xcd_logical(slot, gridDim.x, n_work), NHP, e_local, s_tp, e, hp, mt);
+    decode_work(L, NHP, e_local, s_tp, e, hp, mt);
     const int m0 = mt * BM;
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
-    for (int r = tid; r < BM; r += TNT) {
+    for (int r = tid; r < BM; r += G::NT) {
       const int rr = rb + (r < rows ? r : 0);
       s_rowoff[r] = (long long)rr * I;
       s_soff[r] = rr * IB;
@@ -379,65 +444,69 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     __syncthreads();
 
     const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
-    const bool active = G::CG == 1 || wc * CW * 16 < rows;
+    const int ncc = __builtin_amdgcn_readfirstlane(min(CW, max(0, (rows - wc * CW * 16 + 15) >> 4)));
     const int g0 = wr * WT;  // first of this wave's 16 row tiles
     const int hb = 2 * hp + (g0 >> 3), t0 = g0 & 7;
     // scale pair component (g0 >> 3) is this wave's H block
     const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15)) + (g0 >> 3);
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
     const float* ws0_p = w2s + (size_t)(e * HB + 2 * hp) * IB;  // H block 2hp; 2hp+1 follows at +IB
-    v8i wf[WS][WT];
-    auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane); };
-    v4f acc[WT][CW];
+    with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
+      constexpr int NC = decltype(nct)::value;
+      v8i wf[WS][WT];
+      auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane); };
+      v4f acc[WT][CW];
 #pragma unroll
-    for (int t = 0; t < WT; ++t)
+      for (int t = 0; t < WT; ++t)
 #pragma unroll
-      for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
-    MmaPipe<WT, CW, NSC> pipe;
+        for (int cc = 0; cc < CW; ++cc) acc[t][cc] = zero4;
+      MmaPipe<WT, CW, NSC> pipe;
 
-    ActStage<CT, RW> st[AS];
+      ActStage<CT, RW, NW> st[AS];
 #pragma unroll
-    for (int w0 = 0; w0 < WS - 1; ++w0)
+      for (int w0 = 0; w0 < WS - 1; ++w0)
 #pragma unroll
-      for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
+        for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
-    for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq, s_rowoff, (size_t)a0 * BLK, Cs, s_soff, (size_t)a0, tid);
-    st[0].store(s_act, s_scl, 0, tid, ws0_p[0], ws0_p[IB]);
-    st[0].load(Cq, s_rowoff, (size_t)AS * BLK, Cs, s_soff, (size_t)AS, tid);
+      for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq, s_rowoff, (size_t)a0 * BLK, Cs, s_soff, (size_t)a0, tid);
+      st[0].store(s_act, s_scl, 0, tid, ws0_p[0], ws0_p[IB]);
+      st[0].load(Cq, s_rowoff, (size_t)AS * BLK, Cs, s_soff, (size_t)AS, tid);
 
 #pragma unroll 1
-    for (int kb0 = 0; kb0 < IB; kb0 += 4) {
+      for (int kb0 = 0; kb0 < IB; kb0 += 4) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int kb = kb0 + s;
-        step_barrier();
-        const int kw = min(kb + WS - 1, IB - 1);
-        const int ka = min(kb + AS + 1, IB - 1);
-        const int k1 = min(kb + 1, IB - 1);
-        const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
-        const float* asp = ascl + (s & 1) * 2 * BM;
+        for (int s = 0; s < 4; ++s) {
+          const int kb = kb0 + s;
+          step_barrier();
+          const int kw = min(kb + WS - 1, IB - 1);
+          const int ka = min(kb + AS + 1, IB - 1);
+          const int k1 = min(kb + 1, IB - 1);
+          const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
+          const float* asp = ascl + (s & 1) * 2 * G::NT;
 #pragma unroll
-        for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-        if (active) pipe.step(s, acc, wf[s % WS], af, asp, kb == 0);
-        st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, ws0_p[k1], ws0_p[IB + k1]);
-        st[(s + 1) % AS].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
-      }
-    }
-    if (active) pipe.drain(acc);
-
-#pragma unroll
-    for (int cc = 0; cc < CW; ++cc) {
-      const int row = (wc * CW + cc) * 16 + (lane & 15);
-      if (row < rows) {
-        const float rw = route_weight[rb + row];
-        float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
-#pragma unroll
-        for (int t = 0; t < WT; ++t) {
-          const v4f y = acc[t][cc] * rw;
-          *reinterpret_cast<float4*>(yrow + 16 * t) = make_float4(y[0], y[1], y[2], y[3]);
+          for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
+          if constexpr (NC > 0) pipe.template step<NC>(s, acc, wf[s % WS], af, asp, kb == 0);
+          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, ws0_p[k1], ws0_p[IB + k1]);
+          __builtin_amdgcn_sched_barrier(0);
+          st[(s + 1) % AS].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
         }
       }
-    }
+      if constexpr (NC > 0) pipe.template drain<NC>(acc);
+
+#pragma unroll
+      for (int cc = 0; cc < NC; ++cc) {
+        const int row = (wc * CW + cc) * 16 + (lane & 15);
+        if (row < rows) {
+          const float rw = route_weight[rb + row];
+          float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+#pragma unroll
+          for (int t = 0; t < WT; ++t) {
+            const v4f y = acc[t][cc] * rw;
+            *reinterpret_cast<float4*>(yrow + 16 * t) = make_float4(y[0], y[1], y[2], y[3]);
+          }
+        }
+      }
+    });
     __syncthreads();
   }
 }
@@ -450,27 +519,27 @@ TileShape tile_shape(int T) {
   return expected <= 64 ? TILE_64x256 : (expected <= 128 ? TILE_128x256 : TILE_192x256);
 }
 
-template <int CT, int RW, int WS, int AS>
+template <int CT, int RW, int WS, int AS, int NW>
 hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
                            const int32_t* counts, const int32_t* offsets, const int32_t* route_token, uint8_t* Cq,
-                           float* Cs, int T, int e_local, int max_routes, hipStream_t stream) {
-  constexpr int BM = TileGeom<CT, RW>::BM;
-  auto k = stage1_tile_kernel<CT, RW, WS, AS>;
-  const long long bound = ((long long)e_local + max_routes / BM + 1) * IB;
-  const int grid = persistent_grid(bound, resident_blocks(k, TNT));
-  k<<<grid, TNT, 0, stream>>>(hidden, hs, w13p, w13s, counts, offsets, route_token, Cq, Cs, T, e_local);
+                           float* Cs, int T, int e_local, int max_routes, int32_t* queue, hipStream_t stream) {
+  using G = TileGeom<CT, RW, NW>;
+  auto k = stage1_tile_kernel<CT, RW, WS, AS, NW>;
+  const long long bound = ((long long)e_local + max_routes / G::BM + 1) * IB;
+  const int grid = persistent_grid(bound, resident_blocks(k, G::NT));
+  k<<<grid, G::NT, 0, stream>>>(hidden, hs, w13p, w13s, counts, offsets, route_token, Cq, Cs, T, e_local, queue);
   return hipGetLastError();
 }
 
-template <int CT, int RW, int WS, int AS>
+template <int CT, int RW, int WS, int AS, int NW>
 hipError_t run_stage2_tile(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2s,
                            const int32_t* counts, const int32_t* offsets, const float* rw, float* Y, int e_local,
-                           int max_routes, hipStream_t stream) {
-  constexpr int BM = TileGeom<CT, RW>::BM;
-  auto k = stage2_tile_kernel<CT, RW, WS, AS>;
-  const long long bound = ((long long)e_local + max_routes / BM + 1) * (HB / 2);
-  const int grid = persistent_grid(bound, resident_blocks(k, TNT));
-  k<<<grid, TNT, 0, stream>>>(Cq, Cs, w2p, w2s, counts, offsets, rw, Y, e_local);
+                           int max_routes, int32_t* queue, hipStream_t stream) {
+  using G = TileGeom<CT, RW, NW>;
+  auto k = stage2_tile_kernel<CT, RW, WS, AS, NW>;
+  const long long bound = ((long long)e_local + max_routes / G::BM + 1) * (HB / 2);
+  const int grid = persistent_grid(bound, resident_blocks(k, G::NT));
+  k<<<grid, G::NT, 0, stream>>>(Cq, Cs, w2p, w2s, counts, offsets, rw, Y, e_local, queue);
   return hipGetLastError();
 }
 
@@ -479,33 +548,33 @@ hipError_t run_stage2_tile(const uint8_t* Cq, const float* Cs, const uint8_t* w2
 hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local, int max_routes,
-                         hipStream_t stream) {
+                         int32_t* queue, hipStream_t stream) {
   switch (tile_shape(T)) {
     case TILE_64x256:
-      return run_stage1_tile<4, 4, 4, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
-                                         T, e_local, max_routes, stream);
+      return run_stage1_tile<4, 4, 4, 2, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                         T, e_local, max_routes, queue, stream);
     case TILE_128x256:
-      return run_stage1_tile<8, 8, 2, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
-                                         T, e_local, max_routes, stream);
+      return run_stage1_tile<8, 8, 2, 2, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                         T, e_local, max_routes, queue, stream);
     default:
-      return run_stage1_tile<12, 8, 2, 1>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
-                                          Cs, T, e_local, max_routes, stream);
+      return run_stage1_tile<12, 8, 2, 1, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
+                                          Cs, T, e_local, max_routes, queue, stream);
   }
 }
 
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y, int T,
-                         int e_local, int max_routes, hipStream_t stream) {
+                         int e_local, int max_routes, int32_t* queue, hipStream_t stream) {
   switch (tile_shape(T)) {
     case TILE_64x256:
-      return run_stage2_tile<4, 4, 4, 2>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                         max_routes, stream);
+      return run_stage2_tile<4, 4, 4, 2, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                         max_routes, queue, stream);
     case TILE_128x256:
-      return run_stage2_tile<8, 8, 2, 2>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                         max_routes, stream);
+      return run_stage2_tile<8, 8, 2, 2, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                         max_routes, queue, stream);
     default:
-      return run_stage2_tile<12, 8, 2, 1>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                          max_routes, stream);
+      return run_stage2_tile<12, 8, 2, 1, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
+                                          max_routes, queue, stream);
   }
 }
 

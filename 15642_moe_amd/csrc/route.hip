@@ -139,8 +139,10 @@ __global__ void __launch_bounds__(DISPATCH_CHUNK)
 dispatch_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T,
                 int e_local, int offset, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
                 int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                int32_t* __restrict__ token_route) {
+                int32_t* __restrict__ token_route, int32_t* __restrict__ queue) {
   constexpr int NWAVE = DISPATCH_CHUNK / 64;
+  // The GEMM launches that follow take work from these counters.
+  if (blockIdx.x == 0 && threadIdx.x < QUEUE_COUNTERS) queue[threadIdx.x] = 0;
   __shared__ int s_pre[NWAVE][MAX_E_LOCAL], s_tot[NWAVE][MAX_E_LOCAL];
   __shared__ int s_base[MAX_E_LOCAL];
   __shared__ int s_wtot[NWAVE][MAX_E_LOCAL], s_woff[NWAVE][MAX_E_LOCAL];
@@ -259,10 +261,10 @@ hipError_t launch_route(const float* logits, const float* bias, float rsf, int T
 
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
-                           int32_t* token_route, hipStream_t stream) {
+                           int32_t* token_route, int32_t* queue, hipStream_t stream) {
   const int grid = T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1;
   dispatch_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, counts, offsets,
-                                                       route_token, route_weight, token_route);
+                                                       route_token, route_weight, token_route, queue);
   return hipGetLastError();
 }
 

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MOE_ABI_VERSION 1
+#define MOE_ABI_VERSION 2
 
 #define MOE_OK 0
 #define MOE_ERR_INVALID_ARG 1 /* bad size, null or misaligned pointer */
@@ -47,6 +47,8 @@ enum moe_ws_buffer {
   MOE_WS_CQ,            /* e4m3  [R, I]  SwiGLU output, block-quantised        */
   MOE_WS_CS,            /* f32   [R, 16] its per-128-block scales              */
   MOE_WS_Y,             /* f32   [R, H]  weighted expert outputs per route     */
+  MOE_WS_QUEUE,         /* int32 [16]    work-queue counters of the prefill GEMMs
+                           (zeroed by the dispatch of every forward)           */
   MOE_WS_NBUF
 };
 /* R = T * min(8, e_local) routes at most. */
