@@ -53,7 +53,7 @@ size_t layout(int T, int e_local, size_t* off) {
       R * moe::I,                  // CQ
       R * moe::IB * 4,             // CS
       R * moe::H * 4,              // Y
-      (size_t)moe::QUEUE_COUNTERS * 4,  // QUEUE
+      ((size_t)moe::QUEUE_COUNTERS + (size_t)moe::dispatch_chunks(T) * moe::MAX_E_LOCAL) * 4,  // QUEUE
   };
   size_t acc = 0;
   for (int b = 0; b < MOE_WS_NBUF; ++b) {
@@ -93,7 +93,7 @@ int route_and_dispatch(const float* logits, const float* bias, float rsf, int of
                                           reinterpret_cast<float*>(ws + off[MOE_WS_ROUTE_WEIGHT]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]), st),
-                     "dispatch_kernel launch"));
+                     "dispatch kernels launch"));
   return MOE_OK;
 }
 
@@ -231,7 +231,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
   } else {
     MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,
                                             route_token, route_weight, token_route, queue, st),
-                       "dispatch_kernel launch"));
+                       "dispatch kernels launch"));
     MOE_TRY(mark(2));
     MOE_TRY(hip_status(moe::launch_stage1(static_cast<const uint8_t*>(hidden), hidden_scale,
                                           static_cast<const uint8_t*>(w13_packed), w13_scale, counts, offsets,

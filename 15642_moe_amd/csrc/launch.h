@@ -8,6 +8,9 @@ namespace moe {
 
 hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
                         float* topk_w, hipStream_t stream);
+// Local dispatch; `queue` = the MOE_WS_QUEUE buffer: QUEUE_COUNTERS work-queue
+// counters (cleared here) followed by dispatch_chunks(T) x MAX_E_LOCAL counts.
+int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream);

@@ -3,9 +3,9 @@
 // route_kernel     : no-aux-loss DeepSeek routing, one wave64 per token
 //                    (semantics of reference/moe_ref.py:81-107; the reference
 //                    kernel is route_dispatch_kernel, kernels/moe.cu:213-329).
-// dispatch_kernel  : deterministic token-ordered compaction of the local
-//                    (token, expert) pairs into per-expert route lists, one
-//                    workgroup per 256-token chunk.
+// dispatch_count_kernel, dispatch_place_kernel : deterministic token-ordered
+//                    compaction of the local (token, expert) pairs into
+//                    per-expert route lists, one workgroup per 256-token chunk.
 // combine_kernel   : per-token sum of the weighted per-route expert outputs in
 //                    ascending expert order, then bf16 RNE (the reference does
 //                    fp32 atomics + bf16_convert_kernel, kernels/moe.cu:682,688-695;
@@ -128,55 +128,88 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   }
 }
 
-// One workgroup per chunk of 256 tokens.  Each workgroup histograms the local
-// picks of all tokens (those before its chunk give its per-expert base) and
-// then ranks its own tokens per expert with wave ballots, so slots follow token
-// order (a stable counting sort) and the dispatch is deterministic.  Route r
-// of expert e lives at offsets[e] + slot.
+// Local dispatch in two passes over chunks of 256 tokens (one workgroup
+// each): dispatch_count_kernel writes every chunk's per-expert pick counts,
+// dispatch_place_kernel sums the counts of the chunks before its own (its
+// per-expert base) and ranks its tokens per expert with wave ballots, so
+// slots follow token order (a stable counting sort) and the dispatch is
+// deterministic.  Route r of expert e lives at offsets[e] + slot.
 constexpr int DISPATCH_CHUNK = 256;
+constexpr int DISPATCH_WAVES = DISPATCH_CHUNK / 64;
+
+// Picks of this thread's token (0 past T) as a local-expert bit mask.
+__device__ __forceinline__ uint32_t chunk_token_mask(const int32_t* __restrict__ topk_ids, int T, int offset,
+                                                     int e_local) {
+  const int t = blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
+  return t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
+}
 
 __global__ void __launch_bounds__(DISPATCH_CHUNK)
-dispatch_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T,
-                int e_local, int offset, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                int32_t* __restrict__ token_route, int32_t* __restrict__ queue) {
-  constexpr int NWAVE = DISPATCH_CHUNK / 64;
+dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T, int e_local, int offset,
+                      int32_t* __restrict__ chunk_counts, int32_t* __restrict__ queue) {
+  __shared__ int s_wtot[DISPATCH_WAVES][MAX_E_LOCAL];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The GEMM launches that follow take work from these counters.
-  if (blockIdx.x == 0 && threadIdx.x < QUEUE_COUNTERS) queue[threadIdx.x] = 0;
-  __shared__ int s_pre[NWAVE][MAX_E_LOCAL], s_tot[NWAVE][MAX_E_LOCAL];
+  if (blockIdx.x == 0 && tid < QUEUE_COUNTERS) queue[tid] = 0;
+  const uint32_t m = chunk_token_mask(topk_ids, T, offset, e_local);
+  for (int e = 0; e < e_local; ++e) {
+    const uint64_t bal = __ballot((m >> e) & 1u);
+    if (lane == 0) s_wtot[wave][e] = __popcll(bal);
+  }
+  __syncthreads();
+  if (tid < e_local) {
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < DISPATCH_WAVES; ++w) c += s_wtot[w][tid];
+    chunk_counts[(size_t)blockIdx.x * MAX_E_LOCAL + tid] = c;
+  }
+}
+
+__global__ void __launch_bounds__(DISPATCH_CHUNK)
+dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T,
+                      int e_local, int offset, const int32_t* __restrict__ chunk_counts,
+                      int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+                      int32_t* __restrict__ route_token, float* __restrict__ route_weight,
+                      int32_t* __restrict__ token_route) {
+  constexpr int NWAVE = DISPATCH_WAVES;
+  __shared__ int s_pre[MAX_E_LOCAL], s_tot[MAX_E_LOCAL];
+  __shared__ int s_part[2][DISPATCH_CHUNK];
   __shared__ int s_base[MAX_E_LOCAL];
   __shared__ int s_wtot[NWAVE][MAX_E_LOCAL], s_woff[NWAVE][MAX_E_LOCAL];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = blockIdx.x * DISPATCH_CHUNK;
-  if (tid < MAX_E_LOCAL) {
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) { s_pre[w][tid] = 0; s_tot[w][tid] = 0; }
-  }
-  __syncthreads();
-  for (int t = tid; t < T; t += DISPATCH_CHUNK) {
-    uint32_t m = local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local);
-    while (m) {
-      const int e = __builtin_ctz(m);
-      m &= m - 1;
-      atomicAdd(&s_tot[wave][e], 1);
-      if (t < c0) atomicAdd(&s_pre[wave][e], 1);
+  const int nchunks = gridDim.x;
+  {  // picks of expert tid % 32 in chunks tid/32, tid/32 + 8, ..., before this chunk and in total
+    constexpr int CSTEP = DISPATCH_CHUNK / MAX_E_LOCAL;
+    const int e = tid % MAX_E_LOCAL;
+    int pre = 0, tot = 0;
+#pragma unroll 4
+    for (int c = tid / MAX_E_LOCAL; c < nchunks; c += CSTEP) {
+      const int v = e < e_local ? chunk_counts[(size_t)c * MAX_E_LOCAL + e] : 0;
+      pre += c < (int)blockIdx.x ? v : 0;
+      tot += v;
     }
+    s_part[0][tid] = pre;
+    s_part[1][tid] = tot;
   }
   __syncthreads();
-  if (tid < MAX_E_LOCAL) {
+  if (tid < e_local) {
     int pre = 0, tot = 0;
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) { pre += s_pre[w][tid]; tot += s_tot[w][tid]; }
-    s_pre[0][tid] = pre;
-    s_tot[0][tid] = tot;
+    for (int j = 0; j < DISPATCH_CHUNK / MAX_E_LOCAL; ++j) {
+      pre += s_part[0][j * MAX_E_LOCAL + tid];
+      tot += s_part[1][j * MAX_E_LOCAL + tid];
+    }
+    s_pre[tid] = pre;
+    s_tot[tid] = tot;
   }
   __syncthreads();
   if (tid == 0) {
     int acc = 0;
     for (int e = 0; e < e_local; ++e) {
-      s_base[e] = acc + s_pre[0][e];
-      if (blockIdx.x == 0) { counts[e] = s_tot[0][e]; offsets[e] = acc; }
-      acc += s_tot[0][e];
+      s_base[e] = acc + s_pre[e];
+      if (blockIdx.x == 0) { counts[e] = s_tot[e]; offsets[e] = acc; }
+      acc += s_tot[e];
     }
     if (blockIdx.x == 0) offsets[e_local] = acc;
   }
@@ -259,12 +292,18 @@ hipError_t launch_route(const float* logits, const float* bias, float rsf, int T
   return hipGetLastError();
 }
 
+int dispatch_chunks(int T) { return T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1; }
+
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream) {
-  const int grid = T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1;
-  dispatch_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, counts, offsets,
-                                                       route_token, route_weight, token_route, queue);
+  const int grid = dispatch_chunks(T);
+  int32_t* chunk_counts = queue + QUEUE_COUNTERS;
+  dispatch_count_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts, queue);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  dispatch_place_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, chunk_counts,
+                                                             counts, offsets, route_token, route_weight, token_route);
   return hipGetLastError();
 }
 

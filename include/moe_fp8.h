@@ -47,8 +47,9 @@ enum moe_ws_buffer {
   MOE_WS_CQ,            /* e4m3  [R, I]  SwiGLU output, block-quantised        */
   MOE_WS_CS,            /* f32   [R, 16] its per-128-block scales              */
   MOE_WS_Y,             /* f32   [R, H]  weighted expert outputs per route     */
-  MOE_WS_QUEUE,         /* int32 [16]    work-queue counters of the prefill GEMMs
-                           (zeroed by the dispatch of every forward)           */
+  MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/256)]  work-queue counters of the
+                           prefill GEMMs (zeroed by the dispatch of every
+                           forward), then the dispatch's per-chunk counts      */
   MOE_WS_NBUF
 };
 /* R = T * min(8, e_local) routes at most. */
