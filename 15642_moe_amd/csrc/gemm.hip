@@ -33,14 +33,47 @@ namespace moe {
 // exit at once.
 // ---------------------------------------------------------------------------
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v8i frag(const u32x4& lo, const u32x4& hi) {
+  return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Loads of the decode K loops are issued from inline assembly (SGPR base +
+// per-lane 32-bit offset, no address arithmetic per K-block) and waited for
+// explicitly: the ring keeps NR-1 K-blocks in flight, one
+// `s_waitcnt vmcnt((NR-1) * loads-per-K-block)` before each K-block's MFMAs,
+// whereas the compiler's own count at the unrolled loop's entry collapses
+// the ring for one K-block in NR.  The registers of the K-block then pass
+// through an empty asm, which orders every use after the wait.  Uniform
+// values (weight-block scales) are loaded the same way rather than by scalar
+// loads, whose waits would cover every outstanding load.
+__device__ __forceinline__ void gload2(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:1024"
+                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gload2_adj(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
+                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gload1(float& x, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dword %0, %1, %2" : "=&v"(x) : "v"(voff), "s"(sbase) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 __device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice) {
   e = p / nslice;
   slice = p - e * nslice;
 }
 
-// Stage 1, one wave per (expert e, gate/up tile pair j): 16 I columns,
+// Stage 1, one wave per (expert e, NPW gate/up tile pairs from j*NPW): 16*NPW
+// I columns (each activation fragment serves 2*NPW weight tiles),
 // c = gate * silu(up) written in fp32 to Cf [R, 2048] (the FP8 requant needs
-// the amax over 128 columns, i.e. 8 items, and runs in quant_kernel).  The
+// the amax over 128 columns, i.e. over several items, and runs in
+// quant_kernel).  The
 // local dispatch is fused into the prologue: every item ranks the T x 8 picks
 // with wave ballots (counts, offsets, its expert's tokens in token order);
 // items j == 0 publish their expert's route arrays, item (0, 0) the counts,
@@ -52,7 +85,7 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
                      const uint8_t* __restrict__ w13p, const float* __restrict__ w13s, int32_t* __restrict__ counts,
                      int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
                      float* __restrict__ route_weight, int32_t* __restrict__ token_route, float* __restrict__ Cf) {
-  constexpr int BM = 16, NPAIR = I / 16;
+  constexpr int BM = 16, NPW = 2, NPAIR = I / 16 / NPW;
   static_assert(HB % NR == 0, "ring depth must divide the K-block count");
   __shared__ int s_tok[DECODE_MAX_T];
   const int lane = threadIdx.x;
@@ -116,7 +149,7 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
   // ---- GEMM1 + SwiGLU for 16-route tiles
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
   const int col = lane & 15;
-  const int nb = j >> 3, pj = j & 7;
+  const int nb = (j * NPW) >> 3, pj = (j * NPW) & 7;
   const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(2 * pj) * TILE_BYTES;
   const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
   const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
@@ -124,40 +157,60 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
     __asm__ volatile("" ::: "memory");  // keep the weight prologue inside the loop
     const int rows = min(BM, my_cnt - m0);
     const int tok = s_tok[m0 + (col < rows ? col : 0)];  // padding columns reuse a real row
-    const uint8_t* arow = hidden + (size_t)tok * H + 32 * (lane >> 4);
-    const float* srow = hscale + tok;
-    v8i wg[NR], wu[NR], bq[NR];
-    float as[NR];
+    const uint32_t avoff = (uint32_t)tok * H + 32 * (lane >> 4), svoff = (uint32_t)tok * 4;
+    const uint32_t wvoff = (uint32_t)lane * 16;
+    // loads per K-block: 2 weight tiles x 2 halves, 2 activation halves, the
+    // activation scale and the two weight-block scales
+    constexpr int LPK = 4 * NPW + 5;
+    u32x4 wgl[NR][NPW], wgh[NR][NPW], wul[NR][NPW], wuh[NR][NPW], bl[NR], bh[NR];
+    float as[NR], sg[NR], su[NR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W13_KB_BYTES;
-      wg[sl] = load_tile_frag(pw, lane);
-      wu[sl] = load_tile_frag(pw + TILE_BYTES, lane);
-      const uint8_t* a = arow + kb * BLK;
-      bq[sl] = make_v8i(*reinterpret_cast<const uint4*>(a), *reinterpret_cast<const uint4*>(a + 16));
-      as[sl] = srow[(size_t)kb * T];
+#pragma unroll
+      for (int p = 0; p < NPW; ++p) {
+        gload2(wgl[sl][p], wgh[sl][p], wvoff, pw + 2 * p * TILE_BYTES);
+        gload2(wul[sl][p], wuh[sl][p], wvoff, pw + (2 * p + 1) * TILE_BYTES);
+      }
+      gload2_adj(bl[sl], bh[sl], avoff, hidden + (size_t)kb * BLK);
+      gload1(as[sl], svoff, hscale + (size_t)kb * T);
+      gload1(sg[sl], 0u, wsg_p + kb);
+      gload1(su[sl], 0u, wsu_p + kb);
     };
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
-    v4f accg = zero4, accu = zero4;
+    v4f accg[NPW], accu[NPW];
+#pragma unroll
+    for (int p = 0; p < NPW; ++p) { accg[p] = zero4; accu[p] = zero4; }
 #pragma unroll 1
     for (int kb0 = 0; kb0 < HB; kb0 += NR) {
 #pragma unroll
       for (int sl = 0; sl < NR; ++sl) {
         const int kb = kb0 + sl;
         issue(min(kb + NR - 1, HB - 1), (sl + NR - 1) % NR);  // branch-free; the tail re-reads a K-block
-        __builtin_amdgcn_sched_barrier(0);
-        accg += mfma_16x16x128_fp8(wg[sl], bq[sl], zero4) * (as[sl] * wsg_p[kb]);
-        accu += mfma_16x16x128_fp8(wu[sl], bq[sl], zero4) * (as[sl] * wsu_p[kb]);
+        wait_vm<LPK * (NR - 1)>();
+#pragma unroll
+        for (int p = 0; p < NPW; ++p) __asm__ volatile("" : "+v"(wgl[sl][p]), "+v"(wgh[sl][p]), "+v"(wul[sl][p]), "+v"(wuh[sl][p]));
+        __asm__ volatile("" : "+v"(bl[sl]), "+v"(bh[sl]), "+v"(as[sl]), "+v"(sg[sl]), "+v"(su[sl]));
+        const v8i bq = frag(bl[sl], bh[sl]);
+#pragma unroll
+        for (int p = 0; p < NPW; ++p) {
+          accg[p] += mfma_16x16x128_fp8(frag(wgl[sl][p], wgh[sl][p]), bq, zero4) * (as[sl] * sg[sl]);
+          accu[p] += mfma_16x16x128_fp8(frag(wul[sl][p], wuh[sl][p]), bq, zero4) * (as[sl] * su[sl]);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    wait_vm<0>();  // the dead tail loads land before the registers are reused
     if (col < rows) {
-      float4 c;
-      c.x = (accu[0] / (1.0f + __expf(-accu[0]))) * accg[0];
-      c.y = (accu[1] / (1.0f + __expf(-accu[1]))) * accg[1];
-      c.z = (accu[2] / (1.0f + __expf(-accu[2]))) * accg[2];
-      c.w = (accu[3] / (1.0f + __expf(-accu[3]))) * accg[3];
-      *reinterpret_cast<float4*>(Cf + (size_t)(my_off + m0 + col) * I + 16 * j + 4 * (lane >> 4)) = c;
+#pragma unroll
+      for (int p = 0; p < NPW; ++p) {
+        float4 c;
+        c.x = (accu[p][0] / (1.0f + __expf(-accu[p][0]))) * accg[p][0];
+        c.y = (accu[p][1] / (1.0f + __expf(-accu[p][1]))) * accg[p][1];
+        c.z = (accu[p][2] / (1.0f + __expf(-accu[p][2]))) * accg[p][2];
+        c.w = (accu[p][3] / (1.0f + __expf(-accu[p][3]))) * accg[p][3];
+        *reinterpret_cast<float4*>(Cf + (size_t)(my_off + m0 + col) * I + 16 * (j * NPW + p) + 4 * (lane >> 4)) = c;
+      }
     }
   }
 }
@@ -216,17 +269,18 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
     const int rows = min(BM, cnt - m0);
     const int rb = off + m0;
     const int r = rb + (col < rows ? col : 0);
-    const uint8_t* arow = Cq + (size_t)r * I + 32 * (lane >> 4);
-    const float* srow = Cs + (size_t)r * IB;
-    v8i wt[NR][4], bq[NR];
-    float as[NR];
+    const uint32_t avoff = (uint32_t)r * I + 32 * (lane >> 4), svoff = (uint32_t)r * IB * 4;
+    const uint32_t wvoff = (uint32_t)lane * 16;
+    constexpr int LPK = 12;  // 4 weight tiles x 2 halves, 2 activation halves, C scale, weight-block scale
+    u32x4 wl[NR][4], wh[NR][4], bl[NR], bh[NR];
+    float as[NR], sw[NR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W2_KB_BYTES;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wt[sl][i] = load_tile_frag(pw + i * TILE_BYTES, lane);
-      const uint8_t* a = arow + kb * BLK;
-      bq[sl] = make_v8i(*reinterpret_cast<const uint4*>(a), *reinterpret_cast<const uint4*>(a + 16));
-      as[sl] = srow[kb];
+      for (int i = 0; i < 4; ++i) gload2(wl[sl][i], wh[sl][i], wvoff, pw + i * TILE_BYTES);
+      gload2_adj(bl[sl], bh[sl], avoff, Cq + (size_t)kb * BLK);
+      gload1(as[sl], svoff, Cs + kb);
+      gload1(sw[sl], 0u, ws_p + kb);
     };
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
@@ -237,15 +291,21 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
       for (int sl = 0; sl < NR; ++sl) {
         const int kb = kb0 + sl;
         issue(min(kb + NR - 1, IB - 1), (sl + NR - 1) % NR);  // branch-free, clamped
-        const float sc = as[sl] * ws_p[kb];
+        wait_vm<LPK * (NR - 1)>();
+        __asm__ volatile("" : "+v"(wl[sl][0]), "+v"(wh[sl][0]), "+v"(wl[sl][1]), "+v"(wh[sl][1]), "+v"(wl[sl][2]),
+                         "+v"(wh[sl][2]), "+v"(wl[sl][3]), "+v"(wh[sl][3]), "+v"(bl[sl]), "+v"(bh[sl]), "+v"(as[sl]),
+                         "+v"(sw[sl]));
+        const float sc = as[sl] * sw[sl];
+        const v8i bq = frag(bl[sl], bh[sl]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           __builtin_amdgcn_sched_barrier(0);
-          acc[i] += mfma_16x16x128_fp8(wt[sl][i], bq[sl], zero4) * sc;
+          acc[i] += mfma_16x16x128_fp8(frag(wl[sl][i], wh[sl][i]), bq, zero4) * sc;
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    wait_vm<0>();
     if (col < rows) {
       const float rw = route_weight[rb + col];
       float* yrow = Y + (size_t)(rb + col) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
@@ -290,7 +350,7 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
                                 float* route_weight, int32_t* token_route, float* Cf, uint8_t* Cq, float* Cs,
                                 hipStream_t stream) {
   if (T > DECODE_MAX_T) return hipErrorInvalidValue;
-  const int grid = e_local * (I / 16);
+  const int grid = e_local * (I / 32);
   stage1_decode_kernel<4><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale, w13p,
                                                    w13_scale, counts, offsets, route_token, route_weight, token_route,
                                                    Cf);
