@@ -18,6 +18,7 @@ MOE_OK = 0
 MOE_ERR_INVALID_ARG = 1
 MOE_ERR_HIP = 2
 MOE_ERR_WORKSPACE = 3
+MAX_T = 262143  # include/moe_fp8.h MOE_MAX_T: 32-bit activation offsets in the grouped GEMMs
 
 # Workspace buffer ids (enum moe_ws_buffer).
 (WS_TOPK_IDS, WS_TOPK_W, WS_COUNTS, WS_OFFSETS, WS_ROUTE_TOKEN, WS_ROUTE_WEIGHT, WS_TOKEN_ROUTE, WS_CQ, WS_CS, WS_Y,

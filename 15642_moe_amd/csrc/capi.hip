@@ -172,7 +172,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
                         const float* bias, float routed_scaling_factor, int local_expert_offset, int T, int e_local,
                         void* workspace, size_t workspace_bytes, void* out_bf16, void* stream,
                         void* const* events, int n_events) {
-  if (T < 0) return fail(MOE_ERR_INVALID_ARG, "T must be >= 0, got %d", T);
+  if (T < 0 || T > MOE_MAX_T) return fail(MOE_ERR_INVALID_ARG, "T must be in [0, %d], got %d", MOE_MAX_T, T);
   MOE_TRY(check_e_local(e_local));
   if (events && n_events < MOE_FORWARD_EVENTS)
     return fail(MOE_ERR_INVALID_ARG, "events needs %d entries, got %d", MOE_FORWARD_EVENTS, n_events);

@@ -56,19 +56,28 @@ struct TileGeom {
 };
 
 // LDS layout of the activation stages: s_act[route tile c][buffer][2 KB]
-// fragment tiles, s_scl[buffer][NT] scale pairs (the first BM used).  A fragment tile has the MFMA
-// operand's split-half layout (chunk (route i, lane-group g, half h) at
-// h*1024 + g*256 + i*16), so lane l reads bytes l*16.. of each half: the
-// reads are lane-contiguous (no bank conflicts on gfx950, where a permuted
-// 16-lane read costs half again as long), and one lane offset serves both
-// halves and every (tile, buffer) through the instruction's immediate offset
-// (c*4096 + buffer*2048 + h*1024 < 64 KB for CT <= 16).
+// fragment tiles, s_scl[buffer][NT] scale pairs (the first BM used).  A
+// fragment tile holds the MFMA operand in split halves: chunk (route i,
+// lane-group g, half h) -- K bytes 32g+16h .. +15 of route i -- at
+// h*1024 + g*256 + i*16, so lane l = 16g+i reads bytes l*16.. of each half.
+// gfx950 serves a ds_read_b128 at full rate only when the lanes' addresses
+// follow lane order (a permuted 16-lane read, even one free of bank
+// conflicts, takes nearly twice as long); the staging stores, whose 8-lane
+// groups each write 8 routes' same chunk (128 contiguous bytes), run
+// without bank conflicts in this layout as well.  The lane's lo and hi
+// offsets serve every (tile, buffer) through the instruction's immediate
+// offset (c*4096 + buffer*2048 < 64 KB for CT <= 16).
 __device__ __forceinline__ int frag_slot(int i, int g, int h) { return h * 1024 + g * 256 + i * 16; }
 
-__device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
-  const uint4 lo = *reinterpret_cast<const uint4*>(p);
-  const uint4 hi = *reinterpret_cast<const uint4*>(p + 1024);
-  return make_v8i(lo, hi);
+__device__ __forceinline__ v8i lds_frag(const uint8_t* lo, const uint8_t* hi) {
+  return make_v8i(*reinterpret_cast<const uint4*>(lo), *reinterpret_cast<const uint4*>(hi));
+}
+
+// Lane k's value of v (k wave-uniform): per-K-block weight scales are held
+// one K-block per lane for the whole item, so the K loop has no scalar loads
+// (whose waits would also drain the wave's LDS reads).
+__device__ __forceinline__ float lane_value(float v, int k) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
 }
 
 // Registers holding one K-block of the route tile on its way to LDS: this
@@ -76,11 +85,42 @@ __device__ __forceinline__ v8i lds_frag(const uint8_t* p) {
 // scale.  Chunk x = tid + i*NT is route 8*(x/64) + x%8, K chunk (x/8)%8: a
 // wave instruction still covers 8 whole 128-byte rows (full cache lines),
 // and its 8-lane groups store 8 routes' same chunk, 128 contiguous LDS bytes
-// (one route's 8 chunks would all fall in one bank group).  Row r's K-block starts at
-// abase + s_rowoff[r] + kofs, its scale at sbase[s_soff[r] + sofs]; padding
-// routes take route 0's offsets (a real row).
+// (one route's 8 chunks would all fall in one bank group).  Row r's K-block
+// starts at abase + kofs + s_rowoff[r], its scale at sbase[sofs + s_soff[r]];
+// padding routes take route 0's offsets (a real row).
 __device__ __forceinline__ int chunk_route(int x) { return ((x >> 6) << 3) | (x & 7); }
 __device__ __forceinline__ int chunk_k(int x) { return (x >> 3) & 7; }
+
+// This thread's gather offsets for the current item, read once from the
+// item's row table: byte offset of each of its chunks within a K-block row
+// set, and the byte offset of route tid's scale.  32-bit offsets (the host
+// bounds T so that every activation offset fits) added to a wave-uniform
+// base: the loads take the scalar-base + 32-bit-offset form, one VGPR per
+// offset and no address arithmetic in the K loop.
+template <int CT, int RW, int NW>
+struct GatherAddr {
+  using G = TileGeom<CT, RW, NW>;
+  uint32_t roff[G::ACH];
+  uint32_t soff;
+  __device__ __forceinline__ void bind(const uint32_t* s_rowoff, const uint32_t* s_soff, int tid) {
+#pragma unroll
+    for (int i = 0; i < G::ACH; ++i) {
+      const int x = tid + i * G::NT;
+      const int r = (G::NCH % G::NT == 0 || x < G::NCH) ? chunk_route(x) : 0;
+      roff[i] = s_rowoff[r] + (uint32_t)(chunk_k(x) * 16);
+    }
+    soff = s_soff[tid < G::BM ? tid : 0] * 4u;
+  }
+};
+
+// A wave-uniform base plus a 32-bit per-lane byte offset.  The empty asm
+// keeps the offset a 32-bit value inside the loop (hoisted out of it, its
+// 64-bit extension would take two VGPRs and a 64-bit add per load).
+template <typename V>
+__device__ __forceinline__ const V* at_offset(const void* base, uint32_t off) {
+  __asm__ volatile("" : "+v"(off));
+  return reinterpret_cast<const V*>(static_cast<const uint8_t*>(base) + off);
+}
 
 template <int CT, int RW, int NW>
 struct ActStage {
@@ -93,16 +133,13 @@ struct ActStage {
   // some path the compiler's vmcnt waits must assume the shorter count, and
   // the first MFMA of a step would then also wait for the previous step's
   // gathers.
-  __device__ __forceinline__ void load_chunk(int i, const uint8_t* __restrict__ abase, const long long* s_rowoff,
-                                             size_t kofs, int tid) {
+  __device__ __forceinline__ void load_chunk(int i, const uint8_t* __restrict__ abase_k,
+                                             const GatherAddr<CT, RW, NW>& ga, int tid) {
     const int x = tid + i * G::NT;
-    v[i] = (G::NCH % G::NT == 0 || x < G::NCH)
-               ? *reinterpret_cast<const uint4*>(abase + s_rowoff[chunk_route(x)] + kofs + chunk_k(x) * 16)
-               : make_uint4(0, 0, 0, 0);
+    v[i] = (G::NCH % G::NT == 0 || x < G::NCH) ? *at_offset<uint4>(abase_k, ga.roff[i]) : make_uint4(0, 0, 0, 0);
   }
-  __device__ __forceinline__ void load_scale(const float* __restrict__ sbase, const int* s_soff, size_t sofs,
-                                             int tid) {
-    sc = sbase[s_soff[tid < G::BM ? tid : 0] + sofs];
+  __device__ __forceinline__ void load_scale(const float* __restrict__ sbase_k, const GatherAddr<CT, RW, NW>& ga) {
+    sc = *at_offset<float>(sbase_k, ga.soff);
   }
   // Into buffer b of s_act [CT][2][TILE_BYTES] / s_scl [2][BM] (scale pairs).
   __device__ __forceinline__ void store_chunk(int i, uint8_t* s_act, int b, int tid) const {
@@ -119,11 +156,12 @@ struct ActStage {
   __device__ __forceinline__ void store_scale(float2* s_scl, int b, int tid, float w0, float w1) const {
     s_scl[b * G::NT + tid] = make_float2(sc * w0, sc * w1);
   }
-  __device__ __forceinline__ void load(const uint8_t* abase, const long long* s_rowoff, size_t kofs,
-                                       const float* sbase, const int* s_soff, size_t sofs, int tid) {
+  // K-block rows at abase_k = activations + K-block offset, scales at sbase_k.
+  __device__ __forceinline__ void load(const uint8_t* abase_k, const float* sbase_k, const GatherAddr<CT, RW, NW>& ga,
+                                       int tid) {
 #pragma unroll
-    for (int i = 0; i < G::ACH; ++i) load_chunk(i, abase, s_rowoff, kofs, tid);
-    load_scale(sbase, s_soff, sofs, tid);
+    for (int i = 0; i < G::ACH; ++i) load_chunk(i, abase_k, ga, tid);
+    load_scale(sbase_k, ga);
   }
   __device__ __forceinline__ void store(uint8_t* s_act, float2* s_scl, int b, int tid, float w0, float w1) const {
 #pragma unroll
@@ -138,7 +176,7 @@ __device__ __forceinline__ void step_barrier() { __asm__ volatile("s_waitcnt lgk
 
 // The MFMA work of one wave over the K-blocks of an item: per K-block and
 // route tile cc, acc[t][cc] += (W_t x B_cc) * scale for its WT weight tiles
-// (wf), with B fragments at af + cc*4096 in LDS and the route's scale
+// (wf), with B fragment halves at afl / afh + cc*4096 in LDS and the route's scale
 // products (activation scale x weight-block scale, formed once per K-block
 // by the staging threads) at asp[cc*32]: with NS == 2 a float2 whose .x
 // serves the even weight tiles and .y the odd ones (gate / up), with NS == 1
@@ -174,17 +212,18 @@ struct MmaPipe {
   // unrolling, so every ring index folds); `first`: the item's first K-block
   // (no earlier route tiles to finish).  NC: route tiles computed (<= CW).
   template <int NC>
-  __device__ __forceinline__ void step(int S, v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* af,
-                                       const float* asp, bool first) {
+  __device__ __forceinline__ void step(int S, v4f (&acc)[WT][CW], const v8i (&wf)[WT], const uint8_t* afl,
+                                       const uint8_t* afh, const float* asp, bool first) {
     static_assert(NC <= CW && NC >= D, "tile count");
     const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
     v8i b[LP + 1];
 #pragma unroll
-    for (int c = 0; c < LP && c < NC; ++c) b[c % (LP + 1)] = lds_frag(af + c * 2 * TILE_BYTES);
+    for (int c = 0; c < LP && c < NC; ++c) b[c % (LP + 1)] = lds_frag(afl + c * 2 * TILE_BYTES, afh + c * 2 * TILE_BYTES);
 #pragma unroll
     for (int cc = 0; cc < NC; ++cc) {
       const int g = S * NC + cc;  // route tile number within the 4-step unroll
-      if (cc + LP < NC) b[(cc + LP) % (LP + 1)] = lds_frag(af + (cc + LP) * 2 * TILE_BYTES);
+      if (cc + LP < NC)
+        b[(cc + LP) % (LP + 1)] = lds_frag(afl + (cc + LP) * 2 * TILE_BYTES, afh + (cc + LP) * 2 * TILE_BYTES);
       if constexpr (NS == 2) a[g % NB] = *reinterpret_cast<const float2*>(asp + cc * 32);
       else a[g % NB].x = asp[cc * 32];
 #pragma unroll
@@ -255,10 +294,10 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
   using G = TileGeom<CT, RW, NW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NP = WT / 2, NSC = 2;
   static_assert(HB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
+  static_assert(HB <= 64, "one K-block scale per lane");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
   __shared__ float2 s_scl[2 * G::NT];
-  __shared__ long long s_rowoff[BM];
-  __shared__ int s_soff[BM];
+  __shared__ uint32_t s_rowoff[BM], s_soff[BM];
   __shared__ float s_red[RW][BM];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
@@ -284,19 +323,23 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     const int rb = s_off[e] + m0;
     for (int r = tid; r < BM; r += G::NT) {
       const int tok = route_token[rb + (r < rows ? r : 0)];
-      s_rowoff[r] = (long long)tok * H;
+      s_rowoff[r] = (uint32_t)tok * H;
       s_soff[r] = tok;
     }
     __syncthreads();
+    GatherAddr<CT, RW, NW> ga;
+    ga.bind(s_rowoff, s_soff, tid);
 
     // This lane's fragment / scale addresses in LDS for route tile wc*CW.
-    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const uint8_t* afl = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const uint8_t* afh = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 1);
     const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15));
     // Route tiles of this wave that hold routes (0 for route groups past the tile's routes).
     const int ncc = __builtin_amdgcn_readfirstlane(min(CW, max(0, (rows - wc * CW * 16 + 15) >> 4)));
     const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
-    const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
-    const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
+    // Gate / up weight-block scales of K-block k in lane k.
+    const float wsg_l = w13s[(size_t)(e * G1B + nb) * HB + min(lane, HB - 1)];
+    const float wsu_l = w13s[(size_t)(e * G1B + IB + nb) * HB + min(lane, HB - 1)];
     // One instantiation of the item body per route-tile count (prologue, K
     // loop and epilogue), so no accumulator crosses between them.
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
@@ -319,9 +362,9 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
       for (int a0 = 0; a0 < AS; ++a0)
-        st[a0].load(hidden, s_rowoff, (size_t)a0 * BLK, hscale, s_soff, (size_t)a0 * T, tid);
-      st[0].store(s_act, s_scl, 0, tid, wsg_p[0], wsu_p[0]);
-      st[0].load(hidden, s_rowoff, (size_t)AS * BLK, hscale, s_soff, (size_t)AS * T, tid);
+        st[a0].load(hidden + (size_t)a0 * BLK, hscale + (size_t)a0 * T, ga, tid);
+      st[0].store(s_act, s_scl, 0, tid, lane_value(wsg_l, 0), lane_value(wsu_l, 0));
+      st[0].load(hidden + (size_t)AS * BLK, hscale + (size_t)AS * T, ga, tid);
 
 #pragma unroll 1
       for (int kb0 = 0; kb0 < HB; kb0 += 4) {
@@ -332,17 +375,18 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
           const int kw = min(kb + WS - 1, HB - 1);  // past the end: dead re-reads of the last block
           const int ka = min(kb + AS + 1, HB - 1);
           const int k1 = min(kb + 1, HB - 1);
-          const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
           const float* asp = ascl + (s & 1) * 2 * G::NT;
           // The next weights, then the MFMAs, then K-block kb+1 (gathered a
           // step ago) from staging set (s+1)%AS into LDS buffer (kb+1)&1 and
           // the gather of K-block kb+AS+1 into the freed set.
 #pragma unroll
           for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-          if constexpr (NC > 0) pipe.template step<NC>(s, acc, wf[s % WS], af, asp, kb == 0);
-          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, wsg_p[k1], wsu_p[k1]);
+          if constexpr (NC > 0)
+            pipe.template step<NC>(s, acc, wf[s % WS], afl + (s & 1) * TILE_BYTES, afh + (s & 1) * TILE_BYTES, asp,
+                                   kb == 0);
+          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, lane_value(wsg_l, k1), lane_value(wsu_l, k1));
           __builtin_amdgcn_sched_barrier(0);  // the set's registers are free only after its stores
-          st[(s + 1) % AS].load(hidden, s_rowoff, (size_t)ka * BLK, hscale, s_soff, (size_t)ka * T, tid);
+          st[(s + 1) % AS].load(hidden + (size_t)ka * BLK, hscale + (size_t)ka * T, ga, tid);
         }
       }
       if constexpr (NC > 0) pipe.template drain<NC>(acc);
@@ -410,10 +454,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   using G = TileGeom<CT, RW, NW>;
   constexpr int BM = G::BM, CW = G::CW, WT = G::WT, NHP = HB / 2, NSC = 1;
   static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
+  static_assert(2 * IB <= 64, "one K-block scale per lane");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
   __shared__ float2 s_scl[2 * G::NT];
-  __shared__ long long s_rowoff[BM];
-  __shared__ int s_soff[BM];
+  __shared__ uint32_t s_rowoff[BM], s_soff[BM];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -438,19 +482,23 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const int rb = s_off[e] + m0;
     for (int r = tid; r < BM; r += G::NT) {
       const int rr = rb + (r < rows ? r : 0);
-      s_rowoff[r] = (long long)rr * I;
-      s_soff[r] = rr * IB;
+      s_rowoff[r] = (uint32_t)rr * I;
+      s_soff[r] = (uint32_t)rr * IB;
     }
     __syncthreads();
+    GatherAddr<CT, RW, NW> ga;
+    ga.bind(s_rowoff, s_soff, tid);
 
-    const uint8_t* afrag = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const uint8_t* afl = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 0);
+    const uint8_t* afh = s_act + (wc * CW) * 2 * TILE_BYTES + frag_slot(lane & 15, lane >> 4, 1);
     const int ncc = __builtin_amdgcn_readfirstlane(min(CW, max(0, (rows - wc * CW * 16 + 15) >> 4)));
     const int g0 = wr * WT;  // first of this wave's 16 row tiles
     const int hb = 2 * hp + (g0 >> 3), t0 = g0 & 7;
     // scale pair component (g0 >> 3) is this wave's H block
     const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15)) + (g0 >> 3);
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
-    const float* ws0_p = w2s + (size_t)(e * HB + 2 * hp) * IB;  // H block 2hp; 2hp+1 follows at +IB
+    // Scales of H block 2hp, K-block k in lane k; of H block 2hp+1 in lane IB + k.
+    const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
       constexpr int NC = decltype(nct)::value;
       v8i wf[WS][WT];
@@ -468,9 +516,9 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 #pragma unroll
         for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
-      for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq, s_rowoff, (size_t)a0 * BLK, Cs, s_soff, (size_t)a0, tid);
-      st[0].store(s_act, s_scl, 0, tid, ws0_p[0], ws0_p[IB]);
-      st[0].load(Cq, s_rowoff, (size_t)AS * BLK, Cs, s_soff, (size_t)AS, tid);
+      for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq + (size_t)a0 * BLK, Cs + a0, ga, tid);
+      st[0].store(s_act, s_scl, 0, tid, lane_value(ws_l, 0), lane_value(ws_l, IB));
+      st[0].load(Cq + (size_t)AS * BLK, Cs + AS, ga, tid);
 
 #pragma unroll 1
       for (int kb0 = 0; kb0 < IB; kb0 += 4) {
@@ -481,14 +529,15 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
           const int kw = min(kb + WS - 1, IB - 1);
           const int ka = min(kb + AS + 1, IB - 1);
           const int k1 = min(kb + 1, IB - 1);
-          const uint8_t* af = afrag + (s & 1) * TILE_BYTES;
           const float* asp = ascl + (s & 1) * 2 * G::NT;
 #pragma unroll
           for (int t = 0; t < WT; ++t) wf[(s + WS - 1) % WS][t] = wtile(kw, t);
-          if constexpr (NC > 0) pipe.template step<NC>(s, acc, wf[s % WS], af, asp, kb == 0);
-          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, ws0_p[k1], ws0_p[IB + k1]);
+          if constexpr (NC > 0)
+            pipe.template step<NC>(s, acc, wf[s % WS], afl + (s & 1) * TILE_BYTES, afh + (s & 1) * TILE_BYTES, asp,
+                                   kb == 0);
+          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, lane_value(ws_l, k1), lane_value(ws_l, IB + k1));
           __builtin_amdgcn_sched_barrier(0);
-          st[(s + 1) % AS].load(Cq, s_rowoff, (size_t)ka * BLK, Cs, s_soff, (size_t)ka, tid);
+          st[(s + 1) % AS].load(Cq + (size_t)ka * BLK, Cs + ka, ga, tid);
         }
       }
       if constexpr (NC > 0) pipe.template drain<NC>(acc);

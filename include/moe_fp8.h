@@ -34,6 +34,9 @@ extern "C" {
 #define MOE_E_GLOBAL 256
 #define MOE_TOP_K 8
 #define MOE_MAX_E_LOCAL 32
+/* Largest T moe_forward accepts: the grouped GEMMs address activation rows
+   with 32-bit offsets (T * 8 routes * MOE_I bytes < 2^32). */
+#define MOE_MAX_T 262143
 
 /* Buffers inside the forward workspace (see moe_workspace_offsets). */
 enum moe_ws_buffer {
@@ -94,7 +97,8 @@ int moe_workspace_offsets(int T, int e_local, size_t* offsets, int n);
  *   w2_packed     moe_pack_w2 output        w2_scale     f32 [e_local, 56, 16]
  *   logits        f32 [T, 256]              bias         f32 [256]
  *   out_bf16      bf16 [T, 7168]
- * All pointers 16-byte aligned.  T == 0 is a no-op.
+ * All pointers 16-byte aligned.  T == 0 is a no-op; T > MOE_MAX_T is
+ * MOE_ERR_INVALID_ARG.
  * Replaces moe_forward (kernels/moe.cu:744-900; binding :907-908).
  */
 int moe_forward(const void* hidden, const float* hidden_scale, const void* w13_packed, const float* w13_scale,

@@ -86,6 +86,13 @@ def test_forward_rejects_negative_T(lib, capi):
     assert "T must be" in _err(lib)
 
 
+def test_forward_rejects_T_past_max(lib, capi):
+    header = (REPO / "include" / "moe_fp8.h").read_text()
+    assert f"#define MOE_MAX_T {capi.MAX_T}" in header
+    assert _forward(lib, T=capi.MAX_T + 1) == capi.MOE_ERR_INVALID_ARG
+    assert "T must be" in _err(lib)
+
+
 def test_forward_T0_is_noop(lib, capi):
     assert _forward(lib, T=0, hidden=None) == capi.MOE_OK
 
