@@ -22,7 +22,7 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "lib15642_moe_fp8.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["route.hip", "pack.hip", "gemm.hip", "prefill.hip", "capi.hip"]
+SOURCES = ["route.hip", "pack.hip", "gemm.hip", "prefill.hip", "upstream.hip", "capi.hip"]
 ARCH = "gfx950"
 
 

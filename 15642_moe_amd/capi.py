@@ -51,6 +51,11 @@ SIGNATURES = {
          _c_vp, _c_vp, ctypes.POINTER(_c_vp), _c_int],
     ),
     "moe_route": (_c_int, [_c_vp, _c_vp, _c_float, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
+    "moe_packed_router_bytes": (_c_size, []),
+    "moe_pack_router": (_c_int, [_c_vp, _c_vp, _c_vp]),
+    "moe_unpack_router": (_c_int, [_c_vp, _c_vp, _c_vp]),
+    "moe_router_workspace_bytes": (_c_size, [_c_int]),
+    "moe_router_quant": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp, _c_size, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_fill_normal_e4m3": (_c_int, [_c_vp, _c_size, _c_u64, _c_u64, _c_vp]),
     "moe_mfma_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
     "moe_host_fill_normal_e4m3": (_c_int, [_c_vp, _c_size, _c_u64, _c_u64, _c_u64, _c_int]),

@@ -276,6 +276,54 @@ int moe_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id,
                     "fill_normal_e4m3_kernel launch");
 }
 
+size_t moe_packed_router_bytes(void) { return (size_t)moe::E_GLOBAL * moe::H * 2; }
+
+int moe_pack_router(const void* router_w_bf16, void* router_packed, void* stream) {
+  MOE_TRY(check_ptr(router_w_bf16, "router_w"));
+  MOE_TRY(check_ptr(router_packed, "router_packed"));
+  return hip_status(moe::launch_pack_router(static_cast<const uint8_t*>(router_w_bf16),
+                                            static_cast<uint8_t*>(router_packed), false,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    "pack_router_kernel launch");
+}
+
+int moe_unpack_router(const void* router_packed, void* router_w_bf16, void* stream) {
+  MOE_TRY(check_ptr(router_packed, "router_packed"));
+  MOE_TRY(check_ptr(router_w_bf16, "router_w"));
+  return hip_status(moe::launch_pack_router(static_cast<const uint8_t*>(router_w_bf16),
+                                            const_cast<uint8_t*>(static_cast<const uint8_t*>(router_packed)), true,
+                                            reinterpret_cast<hipStream_t>(stream)),
+                    "pack_router_kernel launch");
+}
+
+size_t moe_router_workspace_bytes(int T) {
+  if (T <= 0 || T > MOE_MAX_T) return 0;
+  return moe::router_partial_bytes(T);
+}
+
+int moe_router_quant(const void* hidden_bf16, const void* router_packed, int T, void* workspace,
+                     size_t workspace_bytes, float* logits, void* hidden_fp8, float* hidden_scale, void* stream) {
+  if (T < 0 || T > MOE_MAX_T) return fail(MOE_ERR_INVALID_ARG, "T must be in [0, %d], got %d", MOE_MAX_T, T);
+  if (T == 0) return MOE_OK;
+  MOE_TRY(check_ptr(hidden_bf16, "hidden"));
+  MOE_TRY(check_ptr(router_packed, "router_packed"));
+  MOE_TRY(check_ptr(logits, "logits"));
+  MOE_TRY(check_ptr(hidden_fp8, "hidden_fp8"));
+  MOE_TRY(check_ptr(hidden_scale, "hidden_scale"));
+  const size_t need = moe::router_partial_bytes(T);
+  if (need > 0) {
+    MOE_TRY(check_ptr(workspace, "workspace"));
+    if (workspace_bytes < need)
+      return fail(MOE_ERR_WORKSPACE, "workspace has %zu bytes, needs %zu", workspace_bytes, need);
+  }
+  return hip_status(moe::launch_router_quant(static_cast<const uint8_t*>(hidden_bf16),
+                                             static_cast<const uint8_t*>(router_packed), T,
+                                             static_cast<float*>(workspace), logits,
+                                             static_cast<uint8_t*>(hidden_fp8), hidden_scale,
+                                             reinterpret_cast<hipStream_t>(stream)),
+                    "router_quant_kernel launch");
+}
+
 int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream) {
   if (n < 0) return fail(MOE_ERR_INVALID_ARG, "n must be >= 0, got %d", n);
   if (n == 0) return MOE_OK;

@@ -44,6 +44,14 @@ hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_
                                 const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
                                 int e_local, hipStream_t stream);
 
+// Producer of the forward's inputs (router logits + FP8 activations) from
+// bf16 hidden states; `partial` holds router_partial_bytes(T) (unused when 0).
+int router_k_parts(int T);
+size_t router_partial_bytes(int T);
+hipError_t launch_pack_router(const uint8_t* w, uint8_t* packed, bool unpack, hipStream_t stream);
+hipError_t launch_router_quant(const uint8_t* hidden_bf16, const uint8_t* router_packed, int T, float* partial,
+                               float* logits, uint8_t* hidden_fp8, float* hidden_scale, hipStream_t stream);
+
 hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n, hipStream_t stream);
 
 }  // namespace moe

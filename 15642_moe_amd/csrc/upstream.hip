@@ -1,0 +1,245 @@
+// Producer of the forward's inputs, in one pass over the bf16 hidden states:
+//
+//   logits[t, e]      = sum_h x[t, h] * w[e, h]          fp32 accumulation
+//   scale[kb, t]      = max(amax(|x[t, 128 kb .. +128]|) / 448, 1e-8)
+//   hidden_fp8[t, h]  = e4m3_rne(clamp(x[t, h] / scale, -448, 448))
+//
+// i.e. the router GEMM in front of the routing (reference/moe_ref.py:81-85
+// takes its output) and the per-(token, 128-column) dynamic FP8 quantisation
+// whose outputs the forward dequantises (moe_ref.py:58-61, scale layout
+// [56, T]).  The reference has no producer: its inputs come from a random
+// builder (moe_layer.py:45-75).  The quantisation rule is the path's own
+// requant rule (kernels/moe.cu:516-541).
+//
+// One workgroup covers 64 tokens x 64 experts (a quarter of the router) x a
+// range of K-blocks.  Per 128-column K-block its 256 threads gather the 64
+// token rows (16 lanes per row: two whole cache lines), the block is staged
+// in LDS in the B-operand layout of v_mfma_f32_16x16x32_bf16, and each wave
+// multiplies it with its 16-expert tile of the packed router weight (A
+// operand, streamed from L2: the whole weight is 3.5 MiB).  Each of the four
+// expert-quarter workgroups of a token tile also quantises 16 of its rows
+// (the 16 lanes of a row hold the whole 128-column block, so the amax is a
+// 16-lane shuffle reduction).  Loads run three K-blocks ahead through a
+// 4-slot register ring.  Small T splits K over workgroups; their partial
+// sums are added in K order by a second kernel, so the logits are
+// deterministic.
+#include "common.h"
+#include "launch.h"
+
+namespace moe {
+namespace {
+
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int RQ_TOK = 64;                       // tokens per workgroup (4 tiles of 16)
+constexpr int RQ_EQ = 4;                         // expert quarters (64 experts each)
+constexpr int RQ_NT = 256;                       // 4 waves; wave w owns expert tile 4*quarter + w
+constexpr int RQ_NR = 4;                         // register ring depth (K-blocks)
+constexpr int RQ_KS = BLK / 32;                  // MFMA K steps per 128-column block
+constexpr int RQ_FRAG = 1024;                    // one 16 x 32 bf16 operand fragment
+constexpr size_t ROUTER_KB_BYTES = (size_t)RQ_KS * 16 * RQ_FRAG;  // 64 KB per K-block
+constexpr int ROUTER_CHUNKS = E_GLOBAL * H / 8;  // 16-byte chunks of the router weight
+
+// Packed router weight: [kb 56][ks 4][expert tile 16][lane 64][8 bf16]; lane
+// l = 16g + i holds expert 16*tile + i, K = 128 kb + 32 ks + 8g .. +8: the A
+// operand of v_mfma_f32_16x16x32_bf16, one contiguous 1 KB per fragment.
+__global__ void __launch_bounds__(256)
+pack_router_kernel(const uint4* __restrict__ in, uint4* __restrict__ out, int unpack) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= ROUTER_CHUNKS) return;
+  const int lane = d & 63, tile = (d >> 6) & 15, ks = (d >> 10) & 3, kb = d >> 12;
+  const int e = 16 * tile + (lane & 15), k = kb * BLK + ks * 32 + 8 * (lane >> 4);
+  const int s = (e * H + k) >> 3;
+  if (unpack) out[s] = in[d];
+  else out[d] = in[s];
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __builtin_bit_cast(float, u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xFFFF0000u); }
+
+// max over the 16 lanes of a row (DPP: quad permutes, then rotations by 4
+// and 8 within the row), no LDS round trip.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float m) {
+  m = fmaxf(m, dpp_f<0xB1>(m));   // quad_perm [1,0,3,2]
+  m = fmaxf(m, dpp_f<0x4E>(m));   // quad_perm [2,3,0,1]
+  m = fmaxf(m, dpp_f<0x124>(m));  // row_ror:4
+  m = fmaxf(m, dpp_f<0x128>(m));  // row_ror:8
+  return m;
+}
+
+// LDS slot of the B fragment (token tile tt, K step ks) for token i, chunk
+// g: fragment lane 16g + i, stored at position 16g + (i ^ (c & 7)) with
+// c = 4 ks + g.  The XOR spreads the 8 chunks of one token -- which one
+// 8-lane group of a staging store writes -- over 8 bank groups (without it
+// they all share one); the MFMA read becomes a permuted 16-lane read.
+__device__ __forceinline__ uint32_t bslot(int tt, int ks, int g, int i) {
+  const int c = 4 * ks + g;
+  return (uint32_t)(((tt * RQ_KS + ks) * 64 + g * 16 + (i ^ (c & 7))) * 16);
+}
+
+// Workgroup (token tile, expert quarter eq, K part kp): K-blocks kp*kpb ..
+// kp*kpb + kpb - 1.  out = logits [T, 256] when n_kp == 1, else partial sums
+// [n_kp][T][256].  Tokens past T read row T-1 and store nothing.
+__global__ void __launch_bounds__(RQ_NT)
+router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restrict__ wpk, int T, int n_kp,
+                    float* __restrict__ out, uint8_t* __restrict__ hq, float* __restrict__ hs) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_b[2][4 * RQ_KS * RQ_FRAG];  // 2 x 16 KB
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kp = blockIdx.x % n_kp, eq = (blockIdx.x / n_kp) % RQ_EQ, tile = blockIdx.x / (RQ_EQ * n_kp);
+  const int kpb = HB / n_kp, kb0 = kp * kpb;
+  const int t0 = tile * RQ_TOK;
+
+  // This thread's 4 chunks of a 64-token x 128-column block: chunk x =
+  // tid + 256 i is token x/16, columns 8*(x%16) .. +8 (16 bytes of bf16).
+  uint32_t goff[4], sslot[4];
+  int tok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int x = tid + RQ_NT * i, r = x >> 4, c = x & 15;
+    tok[i] = t0 + r;
+    goff[i] = (uint32_t)min(tok[i], T - 1) * (H * 2) + c * 16;
+    sslot[i] = bslot(r >> 4, c >> 2, c & 3, r & 15);
+  }
+  uint32_t rslot[RQ_KS];  // this lane's fragment position for each K step (token tile 0)
+#pragma unroll
+  for (int ks = 0; ks < RQ_KS; ++ks) rslot[ks] = bslot(0, ks, lane >> 4, lane & 15);
+  const uint8_t* wbase = wpk + (size_t)(eq * 4 + w) * RQ_FRAG + lane * 16;
+
+  const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
+  v4f acc[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) acc[tt] = zero4;
+
+  uint4 v[RQ_NR][4], a[RQ_NR][RQ_KS];
+  auto load = [&](int kb, int sl) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[sl][i] = *reinterpret_cast<const uint4*>(hidden + goff[i] + (size_t)kb * (BLK * 2));
+#pragma unroll
+    for (int ks = 0; ks < RQ_KS; ++ks)
+      a[sl][ks] = *reinterpret_cast<const uint4*>(wbase + (size_t)kb * ROUTER_KB_BYTES + ks * (16 * RQ_FRAG));
+  };
+#pragma unroll
+  for (int sl = 0; sl < RQ_NR - 1; ++sl) load(kb0 + sl, sl);
+#pragma unroll 1
+  for (int kq = 0; kq < kpb; kq += RQ_NR) {
+#pragma unroll
+    for (int sl = 0; sl < RQ_NR; ++sl) {
+      const int kb = kb0 + kq + sl;
+      load(min(kb + RQ_NR - 1, kb0 + kpb - 1), (sl + RQ_NR - 1) % RQ_NR);  // branch-free; the tail re-reads
+      {
+        // FP8 quantisation of this workgroup's 16 rows of the block (chunk
+        // set i == eq): the 16 lanes of a token hold its 128 columns.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (i != eq) continue;
+          const uint4 u = v[sl][i];
+          float f[8] = {bf16_lo(u.x), bf16_hi(u.x), bf16_lo(u.y), bf16_hi(u.y),
+                        bf16_lo(u.z), bf16_hi(u.z), bf16_lo(u.w), bf16_hi(u.w)};
+          float m = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(f[q]));
+          m = row16_max(m);
+          const float s = fmaxf(m / E4M3_MAX, 1.0e-8f);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(f[q] / s, -E4M3_MAX), E4M3_MAX);
+          if (tok[i] < T) {
+            const int c = (tid + RQ_NT * i) & 15;
+            uint2 codes;
+            codes.x = cvt2_e4m3(f[0], f[1]) | (cvt2_e4m3(f[2], f[3]) << 16);
+            codes.y = cvt2_e4m3(f[4], f[5]) | (cvt2_e4m3(f[6], f[7]) << 16);
+            *reinterpret_cast<uint2*>(hq + (size_t)tok[i] * H + kb * BLK + c * 8) = codes;
+            if (c == 0) hs[(size_t)kb * T + tok[i]] = s;
+          }
+        }
+      }
+      // Stage the block as B fragments; buffer (kb - kb0) & 1 was last read
+      // two blocks ago, before every wave passed the previous barrier.
+      uint8_t* sb = s_b[sl & 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sb + sslot[i]) = v[sl][i];
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < RQ_KS; ++ks) {
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const v8bf b = *reinterpret_cast<const v8bf*>(sb + rslot[ks] + tt * RQ_KS * RQ_FRAG);
+          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[sl][ks]), b, acc[tt], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  // D layout: lane l holds experts 4*(l/16) .. +3 of token column l%16.
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int t = t0 + tt * 16 + (lane & 15);
+    if (t < T) {
+      const int e = (eq * 4 + w) * 16 + 4 * (lane >> 4);
+      *reinterpret_cast<float4*>(out + ((size_t)kp * T + t) * E_GLOBAL + e) =
+          make_float4(acc[tt][0], acc[tt][1], acc[tt][2], acc[tt][3]);
+    }
+  }
+}
+
+// logits = sum of the K parts' partial sums, added in K order.
+__global__ void __launch_bounds__(256)
+logits_reduce_kernel(const float4* __restrict__ part, int n_kp, int n4, float4* __restrict__ logits) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  float4 s = part[i];
+  for (int k = 1; k < n_kp; ++k) {
+    const float4 p = part[(size_t)k * n4 + i];
+    s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+  }
+  logits[i] = s;
+}
+
+}  // namespace
+
+// K parts per launch: enough workgroups to cover the CUs, each part a
+// multiple of the ring depth in K-blocks.
+int router_k_parts(int T) {
+  const int groups = RQ_EQ * ((T + RQ_TOK - 1) / RQ_TOK);
+  const int parts[] = {1, 2, 7, 14};
+  for (int p : parts)
+    if (groups * p >= 256) return p;
+  return 14;
+}
+
+size_t router_partial_bytes(int T) {
+  const int p = router_k_parts(T);
+  return p > 1 ? (size_t)p * T * E_GLOBAL * sizeof(float) : 0;
+}
+
+hipError_t launch_pack_router(const uint8_t* w, uint8_t* packed, bool unpack, hipStream_t stream) {
+  const int grid = (ROUTER_CHUNKS + 255) / 256;
+  if (unpack)
+    pack_router_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const uint4*>(packed),
+                                                 reinterpret_cast<uint4*>(const_cast<uint8_t*>(w)), 1);
+  else
+    pack_router_kernel<<<grid, 256, 0, stream>>>(reinterpret_cast<const uint4*>(w), reinterpret_cast<uint4*>(packed),
+                                                 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_router_quant(const uint8_t* hidden_bf16, const uint8_t* router_packed, int T, float* partial,
+                               float* logits, uint8_t* hidden_fp8, float* hidden_scale, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  const int n_kp = router_k_parts(T);
+  const int grid = RQ_EQ * n_kp * ((T + RQ_TOK - 1) / RQ_TOK);
+  router_quant_kernel<<<grid, RQ_NT, 0, stream>>>(hidden_bf16, router_packed, T, n_kp, n_kp > 1 ? partial : logits,
+                                                  hidden_fp8, hidden_scale);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || n_kp == 1) return err;
+  const int n4 = T * E_GLOBAL / 4;
+  logits_reduce_kernel<<<(n4 + 255) / 256, 256, 0, stream>>>(reinterpret_cast<const float4*>(partial), n_kp, n4,
+                                                             reinterpret_cast<float4*>(logits));
+  return hipGetLastError();
+}
+
+}  // namespace moe

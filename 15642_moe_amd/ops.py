@@ -107,6 +107,60 @@ def unpack_w2(packed: torch.Tensor) -> torch.Tensor:
     return out
 
 
+# --------------------------------------------------------------------------- upstream producer
+ROUTER_PACKED_SHAPE = (56, 4, 16, 64, 8)  # [kb, ks, expert tile, lane, bf16]
+
+
+def pack_router(router_w: torch.Tensor) -> torch.Tensor:
+    """Router weight bf16 [256, 7168] -> packed bf16 MFMA operand fragments
+    (ROUTER_PACKED_SHAPE), for router_quant."""
+    _require_device("router_w", router_w)
+    _check(router_w.dtype == torch.bfloat16, "router_w must be bfloat16")
+    _check(tuple(router_w.shape) == (E_GLOBAL, H) and router_w.is_contiguous(),
+           "router_w must be [256, 7168] contiguous")
+    out = torch.empty(ROUTER_PACKED_SHAPE, dtype=torch.bfloat16, device=router_w.device)
+    with torch.cuda.device(router_w.device):
+        capi.check(capi.load().moe_pack_router(_ptr(router_w), _ptr(out), _stream(router_w.device)), "pack_router")
+    return out
+
+
+def unpack_router(packed: torch.Tensor) -> torch.Tensor:
+    """Inverse of pack_router."""
+    _require_device("router_packed", packed)
+    _check(tuple(packed.shape) == ROUTER_PACKED_SHAPE and packed.is_contiguous() and packed.dtype == torch.bfloat16,
+           "router_packed must be a pack_router result")
+    out = torch.empty((E_GLOBAL, H), dtype=torch.bfloat16, device=packed.device)
+    with torch.cuda.device(packed.device):
+        capi.check(capi.load().moe_unpack_router(_ptr(packed), _ptr(out), _stream(packed.device)), "unpack_router")
+    return out
+
+
+def router_quant(hidden: torch.Tensor, router_packed: torch.Tensor):
+    """bf16 hidden states [T, 7168] -> (routing_logits f32 [T, 256],
+    hidden_states e4m3 [T, 7168], hidden_states_scale f32 [56, T]): the
+    router GEMM and the dynamic FP8 quantisation in front of moe_forward,
+    in one pass over the hidden states (moe_router_quant)."""
+    _require_device("hidden", hidden)
+    dev = hidden.device
+    _check(hidden.dtype == torch.bfloat16, "hidden must be bfloat16")
+    _check(hidden.dim() == 2 and hidden.size(1) == H and hidden.is_contiguous(), "hidden must be [T, 7168] contiguous")
+    _require_device("router_packed", router_packed, dev)
+    _check(tuple(router_packed.shape) == ROUTER_PACKED_SHAPE and router_packed.dtype == torch.bfloat16,
+           "router_packed must be a pack_router result")
+    T = int(hidden.size(0))
+    _check(T <= capi.MAX_T, f"T must be <= {capi.MAX_T}")
+    lib = capi.load()
+    logits = torch.empty((T, E_GLOBAL), dtype=torch.float32, device=dev)
+    hq = torch.empty((T, H), dtype=torch.float8_e4m3fn, device=dev)
+    hs = torch.empty((H_BLOCKS, T), dtype=torch.float32, device=dev)
+    ws_bytes = int(lib.moe_router_workspace_bytes(T))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        capi.check(lib.moe_router_quant(_ptr(hidden), _ptr(router_packed), T, _ptr(ws), ws_bytes, _ptr(logits),
+                                        _ptr(hq), _ptr(hs), _stream(dev)), "router_quant")
+    return logits, hq, hs
+
+
 # --------------------------------------------------------------------------- forward
 def _validate_forward(hidden, hidden_scale, W13_packed, W13_scale, W2_packed, W2_scale, logits, bias):
     """The checks of kernels/moe.cu:759-817, for this build's packed layout."""

@@ -129,6 +129,29 @@ int moe_route(const float* logits, const float* bias, float routed_scaling_facto
               int T, int e_local, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Producer of moe_forward's activation inputs, one pass over bf16 hidden
+ * states [T, 7168] (the router GEMM and the dynamic FP8 quantisation in
+ * front of the path; the reference has none: its inputs come from a random
+ * builder, moe_layer.py:45-75, and are consumed at moe_ref.py:58-61,81-85):
+ *   logits       f32 [T, 256]   = hidden x router_w^T, fp32 accumulation
+ *   hidden_scale f32 [56, T]    = max(amax(128-column block) / 448, 1e-8)
+ *   hidden_fp8   e4m3 [T, 7168] = RNE(clamp(hidden / scale, +-448))
+ * (the quantisation rule of the path's own requant, kernels/moe.cu:516-541).
+ * router_w bf16 [256, 7168] is packed once by moe_pack_router
+ * (moe_packed_router_bytes() bytes, inverse moe_unpack_router).  The
+ * workspace (moe_router_workspace_bytes(T) bytes, may be 0) holds the
+ * partial sums of small-T launches, which are added in K order: the logits
+ * are deterministic.  All pointers 16-byte aligned; T == 0 is a no-op;
+ * T > MOE_MAX_T is MOE_ERR_INVALID_ARG.
+ */
+size_t moe_packed_router_bytes(void);
+int moe_pack_router(const void* router_w_bf16, void* router_packed, void* stream);
+int moe_unpack_router(const void* router_packed, void* router_w_bf16, void* stream);
+size_t moe_router_workspace_bytes(int T);
+int moe_router_quant(const void* hidden_bf16, const void* router_packed, int T, void* workspace,
+                     size_t workspace_bytes, float* logits, void* hidden_fp8, float* hidden_scale, void* stream);
+
+/*
  * Synthetic e4m3 data, ~N(0,1) (Irwin-Hall of four 16-bit hash fields),
  * bit-identical to the host generator for the same (seed, stream_id).
  * Test/benchmark input synthesis; no counterpart in the reference.
