@@ -11,7 +11,10 @@ too and reported under "configs".  Per-kernel durations come from HIP events
 recorded on the launch stream between the kernels (moe_forward_timed), and
 give the roofline figure of the dominant kernel.  The CPU baseline times the
 oracle's restatement of reference/moe_ref.py (full fp32 dequant, per-expert
-fp32 GEMMs) on the host, on one forward of the same decode batch.
+fp32 GEMMs) on the host, on one forward of the same decode batch.  Under
+"upstream", the producer of the forward's inputs (moe_router_quant: router
+GEMM + dynamic FP8 activation quantisation from bf16 hidden states) is timed
+at each configuration's T.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -190,6 +193,8 @@ def main() -> int:
         del inp, p13, p2, args_fwd, out, ws, evs
         torch.cuda.empty_cache()
 
+    upstream = [_time_upstream(torch, lib, dev, inputs_mod.CONFIGS[i].T, args.steps) for i in cfg_ids]
+
     head = results[inputs_mod.CONFIGS[1].name]
     dom = max(("gemm1_swiglu_quant", "gemm2"), key=lambda k: head["stage_us"][k])
     achieved = head["stage_alg_bytes"][dom] / (head["stage_us"][dom] * 1e-6) / 1e9
@@ -262,9 +267,50 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "configs": results,
+        "upstream": upstream,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _time_upstream(torch, lib, dev, T: int, steps: int) -> dict:
+    """moe_router_quant (router GEMM + FP8 activation quant, the producer of
+    the forward's inputs) at T tokens: synthetic bf16 hidden states and router
+    weight, outputs and workspace allocated once, HIP events around `steps`
+    launches on the current stream."""
+    ops = importlib.import_module("15642_moe_amd.ops")
+    g = torch.Generator(device=dev).manual_seed(0x15642 + T)
+    hidden = torch.randn((T, 7168), generator=g, device=dev).to(torch.bfloat16)
+    router = (torch.randn((256, 7168), generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    packed = ops.pack_router(router)
+    logits = torch.empty((T, 256), dtype=torch.float32, device=dev)
+    hq = torch.empty((T, 7168), dtype=torch.uint8, device=dev)
+    hs = torch.empty((56, T), dtype=torch.float32, device=dev)
+    ws_bytes = int(lib.moe_router_workspace_bytes(T))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    vp = ctypes.c_void_p
+    argv = (vp(hidden.data_ptr()), vp(packed.data_ptr()), T, vp(ws.data_ptr()), ws_bytes, vp(logits.data_ptr()),
+            vp(hq.data_ptr()), vp(hs.data_ptr()), vp(stream.cuda_stream))
+    for _ in range(3):
+        lib.moe_router_quant(*argv)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        rc = lib.moe_router_quant(*argv)
+        if rc:
+            importlib.import_module("15642_moe_amd.capi").check(rc, "moe_router_quant")
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1e3 / steps
+    alg_bytes = T * (7168 * 2 + 7168 + 56 * 4 + 256 * 4) + 256 * 7168 * 2
+    rec = {"kernel": "router_quant_kernel", "T": T, "us": round(us, 2), "alg_bytes": alg_bytes,
+           "hbm_gbs": round(alg_bytes / (us * 1e-6) / 1e9, 1),
+           "tflops": round(2.0 * T * 7168 * 256 / (us * 1e-6) / 1e12, 2)}
+    log(f"upstream T={T}: {json.dumps(rec)}")
+    del hidden, router, packed, logits, hq, hs, ws
+    return rec
 
 
 def _calibrate_copy(torch) -> int:
