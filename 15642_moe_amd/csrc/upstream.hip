@@ -26,6 +26,8 @@
 #include "common.h"
 #include "launch.h"
 
+#include <type_traits>
+
 namespace moe {
 namespace {
 
@@ -71,6 +73,25 @@ __device__ __forceinline__ float row16_max(float m) {
   return m;
 }
 
+// The K loop's memory operations are inline assembly in a fixed order (per
+// K-block: the 8 loads of the block three ahead, then the code store)
+// waited for with explicit counts: the compiler's own waits, merged
+// at the loop head across the unrolled ring and the loop's stores, drained
+// every load there.  The registers of a block pass through an empty asm
+// after its wait, which orders every use after it.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void gload(u32x4& d, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gstore2(uint32_t voff, const u32x2& d, void* sbase) {
+  __asm__ volatile("global_store_dwordx2 %0, %1, %2" :: "v"(voff), "v"(d), "s"(sbase) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 // LDS slot of the B fragment (token tile tt, K step ks) for token i, chunk
 // g: fragment lane 16g + i, stored at position 16g + (i ^ (c & 7)) with
 // c = 4 ks + g.  The XOR spreads the 8 chunks of one token -- which one
@@ -83,97 +104,128 @@ __device__ __forceinline__ uint32_t bslot(int tt, int ks, int g, int i) {
 
 // Workgroup (token tile, expert quarter eq, K part kp): K-blocks kp*kpb ..
 // kp*kpb + kpb - 1.  out = logits [T, 256] when n_kp == 1, else partial sums
-// [n_kp][T][256].  Tokens past T read row T-1 and store nothing.
+// [n_kp][T][256].  Tokens past T read row T-1 and store nothing.  Workgroup
+// p runs on XCD p % 8: token tile t's workgroups all have p % 8 == t % 8, so
+// the four expert quarters that read a token tile's rows share one L2 (dealt
+// round-robin, they would fetch every row into four L2s).  The grid rounds
+// the tile count up to a multiple of 8; workgroups past the last tile exit.
 __global__ void __launch_bounds__(RQ_NT)
 router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restrict__ wpk, int T, int n_kp,
                     float* __restrict__ out, uint8_t* __restrict__ hq, float* __restrict__ hs) {
   __shared__ __attribute__((aligned(16))) uint8_t s_b[2][4 * RQ_KS * RQ_FRAG];  // 2 x 16 KB
+  __shared__ float s_qs[HB][16];  // the quantised rows' scales, written out after the K loop
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kp = blockIdx.x % n_kp, eq = (blockIdx.x / n_kp) % RQ_EQ, tile = blockIdx.x / (RQ_EQ * n_kp);
+  const int q = blockIdx.x / XCDS, rem = q % (RQ_EQ * n_kp);
+  const int tile = (q / (RQ_EQ * n_kp)) * XCDS + blockIdx.x % XCDS, eq = rem / n_kp, kp = rem % n_kp;
+  if (tile * RQ_TOK >= T) return;
   const int kpb = HB / n_kp, kb0 = kp * kpb;
   const int t0 = tile * RQ_TOK;
 
-  // This thread's 4 chunks of a 64-token x 128-column block: chunk x =
-  // tid + 256 i is token x/16, columns 8*(x%16) .. +8 (16 bytes of bf16).
+  // This thread's 4 chunks of a 64-token x 128-column block: chunk i is
+  // token r = tid/16 + 16*((i + eq) % 4), columns 8*(tid%16) .. +8 (16 bytes
+  // of bf16).  Chunk 0 holds the 16 rows this workgroup quantises.
   uint32_t goff[4], sslot[4];
-  int tok[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int x = tid + RQ_NT * i, r = x >> 4, c = x & 15;
-    tok[i] = t0 + r;
-    goff[i] = (uint32_t)min(tok[i], T - 1) * (H * 2) + c * 16;
+    const int r = (tid >> 4) + 16 * ((i + eq) & 3), c = tid & 15;
+    goff[i] = (uint32_t)min(t0 + r, T - 1) * (H * 2) + c * 16;
     sslot[i] = bslot(r >> 4, c >> 2, c & 3, r & 15);
   }
+  // Row this thread quantises (its chunk 0), clamped to T-1.
+  const int qrow = min(t0 + 16 * eq + (tid >> 4), T - 1);
   uint32_t rslot[RQ_KS];  // this lane's fragment position for each K step (token tile 0)
 #pragma unroll
   for (int ks = 0; ks < RQ_KS; ++ks) rslot[ks] = bslot(0, ks, lane >> 4, lane & 15);
-  const uint8_t* wbase = wpk + (size_t)(eq * 4 + w) * RQ_FRAG + lane * 16;
+  const uint8_t* wbase = wpk + (size_t)(eq * 4 + w) * RQ_FRAG;  // + lane*16 per lane
+  const uint32_t wvoff = lane * 16;
+  const uint32_t qoff = (uint32_t)qrow * H + (tid & 15) * 8;
 
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
   v4f acc[4];
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) acc[tt] = zero4;
 
-  uint4 v[RQ_NR][4], a[RQ_NR][RQ_KS];
+  u32x4 v[RQ_NR][4], a[RQ_NR][RQ_KS];
   auto load = [&](int kb, int sl) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[sl][i] = *reinterpret_cast<const uint4*>(hidden + goff[i] + (size_t)kb * (BLK * 2));
+    for (int i = 0; i < 4; ++i) gload(v[sl][i], goff[i], hidden + (size_t)kb * (BLK * 2));
 #pragma unroll
-    for (int ks = 0; ks < RQ_KS; ++ks)
-      a[sl][ks] = *reinterpret_cast<const uint4*>(wbase + (size_t)kb * ROUTER_KB_BYTES + ks * (16 * RQ_FRAG));
+    for (int ks = 0; ks < RQ_KS; ++ks) gload(a[sl][ks], wvoff, wbase + (size_t)kb * ROUTER_KB_BYTES + ks * (16 * RQ_FRAG));
   };
 #pragma unroll
   for (int sl = 0; sl < RQ_NR - 1; ++sl) load(kb0 + sl, sl);
-#pragma unroll 1
-  for (int kq = 0; kq < kpb; kq += RQ_NR) {
+  // One K-block: issue the loads three blocks ahead, wait for this block's
+  // loads, quantise, stage, multiply.  Block kb's loads are older than
+  // exactly WAIT operations: 27 in steady state (its code store, two
+  // K-blocks of 8 loads + 1 store, the 8 loads just issued), 24 / 25 / 26 in
+  // the first three blocks (the prologue loads have no stores between them).
+  int kq = 0;
+  auto step = [&](auto sl_c, auto wait_c) {
+    constexpr int sl = decltype(sl_c)::value, WAIT = decltype(wait_c)::value;
+    const int kb = kb0 + kq + sl;
+    load(min(kb + RQ_NR - 1, kb0 + kpb - 1), (sl + RQ_NR - 1) % RQ_NR);  // branch-free; the tail re-reads
+    wait_vm<WAIT>();
 #pragma unroll
-    for (int sl = 0; sl < RQ_NR; ++sl) {
-      const int kb = kb0 + kq + sl;
-      load(min(kb + RQ_NR - 1, kb0 + kpb - 1), (sl + RQ_NR - 1) % RQ_NR);  // branch-free; the tail re-reads
-      {
-        // FP8 quantisation of this workgroup's 16 rows of the block (chunk
-        // set i == eq): the 16 lanes of a token hold its 128 columns.
+    for (int i = 0; i < 4; ++i) __asm__ volatile("" : "+v"(v[sl][i]));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i != eq) continue;
-          const uint4 u = v[sl][i];
-          float f[8] = {bf16_lo(u.x), bf16_hi(u.x), bf16_lo(u.y), bf16_hi(u.y),
-                        bf16_lo(u.z), bf16_hi(u.z), bf16_lo(u.w), bf16_hi(u.w)};
-          float m = 0.0f;
+    for (int ks = 0; ks < RQ_KS; ++ks) __asm__ volatile("" : "+v"(a[sl][ks]));
+    {
+      // FP8 quantisation of this workgroup's 16 rows of the block (chunk
+      // 0): the 16 lanes of a token hold its 128 columns.  The code store is
+      // unconditional, a fixed operation count for the waits above (rows
+      // past T rewrite row T-1 with the same bytes: they read row T-1); the
+      // scales go to LDS and out after the loop.
+      const u32x4 u = v[sl][0];
+      float f[8] = {bf16_lo(u[0]), bf16_hi(u[0]), bf16_lo(u[1]), bf16_hi(u[1]),
+                    bf16_lo(u[2]), bf16_hi(u[2]), bf16_lo(u[3]), bf16_hi(u[3])};
+      float m = 0.0f;
 #pragma unroll
-          for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(f[q]));
-          m = row16_max(m);
-          const float s = fmaxf(m / E4M3_MAX, 1.0e-8f);
+      for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(f[q]));
+      m = row16_max(m);
+      const float sc = fmaxf(m / E4M3_MAX, 1.0e-8f);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(f[q] / s, -E4M3_MAX), E4M3_MAX);
-          if (tok[i] < T) {
-            const int c = (tid + RQ_NT * i) & 15;
-            uint2 codes;
-            codes.x = cvt2_e4m3(f[0], f[1]) | (cvt2_e4m3(f[2], f[3]) << 16);
-            codes.y = cvt2_e4m3(f[4], f[5]) | (cvt2_e4m3(f[6], f[7]) << 16);
-            *reinterpret_cast<uint2*>(hq + (size_t)tok[i] * H + kb * BLK + c * 8) = codes;
-            if (c == 0) hs[(size_t)kb * T + tok[i]] = s;
-          }
-        }
-      }
-      // Stage the block as B fragments; buffer (kb - kb0) & 1 was last read
-      // two blocks ago, before every wave passed the previous barrier.
-      uint8_t* sb = s_b[sl & 1];
+      for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(f[q] / sc, -E4M3_MAX), E4M3_MAX);
+      u32x2 codes;
+      codes[0] = cvt2_e4m3(f[0], f[1]) | (cvt2_e4m3(f[2], f[3]) << 16);
+      codes[1] = cvt2_e4m3(f[4], f[5]) | (cvt2_e4m3(f[6], f[7]) << 16);
+      gstore2(qoff, codes, hq + (size_t)kb * BLK);
+      if ((tid & 15) == 0) s_qs[kb - kb0][tid >> 4] = sc;
+    }
+    // Stage the block as B fragments; buffer (kb - kb0) & 1 was last read
+    // two blocks ago, before every wave passed the previous barrier.
+    uint8_t* sb = s_b[sl & 1];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(sb + sslot[i]) = v[sl][i];
-      __syncthreads();
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(sb + sslot[i]) = v[sl][i];
+    __syncthreads();
 #pragma unroll
-      for (int ks = 0; ks < RQ_KS; ++ks) {
+    for (int ks = 0; ks < RQ_KS; ++ks) {
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-          const v8bf b = *reinterpret_cast<const v8bf*>(sb + rslot[ks] + tt * RQ_KS * RQ_FRAG);
-          acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[sl][ks]), b, acc[tt], 0, 0, 0);
-        }
+      for (int tt = 0; tt < 4; ++tt) {
+        const v8bf b = *reinterpret_cast<const v8bf*>(sb + rslot[ks] + tt * RQ_KS * RQ_FRAG);
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[sl][ks]), b, acc[tt], 0, 0, 0);
       }
     }
+  };
+  using std::integral_constant;
+  step(integral_constant<int, 0>{}, integral_constant<int, 24>{});
+  step(integral_constant<int, 1>{}, integral_constant<int, 25>{});
+  step(integral_constant<int, 2>{}, integral_constant<int, 26>{});
+  step(integral_constant<int, 3>{}, integral_constant<int, 27>{});
+#pragma unroll 1
+  for (kq = RQ_NR; kq < kpb; kq += RQ_NR) {
+    step(integral_constant<int, 0>{}, integral_constant<int, 27>{});
+    step(integral_constant<int, 1>{}, integral_constant<int, 27>{});
+    step(integral_constant<int, 2>{}, integral_constant<int, 27>{});
+    step(integral_constant<int, 3>{}, integral_constant<int, 27>{});
   }
-
+  wait_vm<0>();  // the dead tail loads land before the registers are reused
+  __syncthreads();
+  // Scales of the 16 quantised rows, [kb][T] layout: 16 consecutive tokens per K-block.
+  for (int j = tid; j < kpb * 16; j += RQ_NT) {
+    const int t = t0 + 16 * eq + (j & 15);
+    if (t < T) hs[(size_t)(kb0 + (j >> 4)) * T + t] = s_qs[j >> 4][j & 15];
+  }
   // D layout: lane l holds experts 4*(l/16) .. +3 of token column l%16.
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
@@ -231,7 +283,8 @@ hipError_t launch_router_quant(const uint8_t* hidden_bf16, const uint8_t* router
                                float* logits, uint8_t* hidden_fp8, float* hidden_scale, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   const int n_kp = router_k_parts(T);
-  const int grid = RQ_EQ * n_kp * ((T + RQ_TOK - 1) / RQ_TOK);
+  const int tiles8 = ((T + RQ_TOK - 1) / RQ_TOK + XCDS - 1) / XCDS * XCDS;
+  const int grid = RQ_EQ * n_kp * tiles8;
   router_quant_kernel<<<grid, RQ_NT, 0, stream>>>(hidden_bf16, router_packed, T, n_kp, n_kp > 1 ? partial : logits,
                                                   hidden_fp8, hidden_scale);
   hipError_t err = hipGetLastError();

@@ -1,6 +1,7 @@
-"""Static check of the inline-assembly loads in the decode GEMM kernels.
+"""Static check of the inline-assembly loads in the decode GEMM kernels and
+the input producer (router_quant_kernel).
 
-gemm.hip issues its K-loop loads from inline assembly and waits for them with
+gemm.hip and upstream.hip issue their K-loop loads from inline assembly and waits for them with
 explicit `s_waitcnt vmcnt(N)`: the compiler does not know those registers are
 still being written.  If register allocation ever moved or reused a load's
 destination before its wait (a copy to another register, a spill, a reuse for
@@ -74,23 +75,34 @@ def check_kernel(lines: list[str]) -> list[str]:
     return problems
 
 
-@pytest.mark.skipif(shutil.which("hipcc") is None and not Path("/opt/rocm/bin/hipcc").exists(),
-                    reason="hipcc not available")
-def test_decode_asm_loads_keep_their_registers():
+def _check_source(source: str, kernel_tag: str) -> int:
     b = importlib.import_module("15642_moe_amd.build")
-    res = subprocess.run([b._hipcc(), *b.compile_flags(), "-S", "--cuda-device-only", str(b.CSRC / "gemm.hip"),
+    res = subprocess.run([b._hipcc(), *b.compile_flags(), "-S", "--cuda-device-only", str(b.CSRC / source),
                           "-o", "-"], capture_output=True, text=True)
     assert res.returncode == 0, res.stderr[-2000:]
     funcs = re.split(r"\n(_ZN\S+):", res.stdout)
     checked = 0
     for k in range(1, len(funcs), 2):
         name, body = funcs[k], funcs[k + 1].split(".Lfunc_end")[0]
-        if "decode_kernel" not in name:
+        if kernel_tag not in name:
             continue
         problems = check_kernel(body.split("\n"))
         assert not problems, f"{name}:\n" + "\n".join(problems[:10])
         checked += 1
-    assert checked == 2
+    return checked
+
+
+HIPCC = shutil.which("hipcc") is not None or Path("/opt/rocm/bin/hipcc").exists()
+
+
+@pytest.mark.skipif(not HIPCC, reason="hipcc not available")
+def test_decode_asm_loads_keep_their_registers():
+    assert _check_source("gemm.hip", "decode_kernel") == 2
+
+
+@pytest.mark.skipif(not HIPCC, reason="hipcc not available")
+def test_router_quant_asm_loads_keep_their_registers():
+    assert _check_source("upstream.hip", "router_quant_kernel") == 1
 
 
 def test_checker_flags_a_moved_destination():
