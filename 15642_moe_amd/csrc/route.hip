@@ -172,15 +172,26 @@ dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
                       int32_t* __restrict__ route_token, float* __restrict__ route_weight,
                       int32_t* __restrict__ token_route) {
   constexpr int NWAVE = DISPATCH_WAVES;
-  __shared__ int s_pre[MAX_E_LOCAL], s_tot[MAX_E_LOCAL];
+  constexpr int CSTEP = DISPATCH_CHUNK / MAX_E_LOCAL;
   __shared__ int s_part[2][DISPATCH_CHUNK];
   __shared__ int s_base[MAX_E_LOCAL];
   __shared__ int s_wtot[NWAVE][MAX_E_LOCAL], s_woff[NWAVE][MAX_E_LOCAL];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = blockIdx.x * DISPATCH_CHUNK;
   const int nchunks = gridDim.x;
+
+  // The token's picks and the chunk counts are loaded up front, so the two
+  // load latencies overlap; nothing below waits on memory again.
+  const int t = c0 + tid;
+  const bool valid = t < T;
+  int ids[TOP_K];
+  float ws[TOP_K];
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k) {
+    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
+    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
+  }
   {  // picks of expert tid % 32 in chunks tid/32, tid/32 + 8, ..., before this chunk and in total
-    constexpr int CSTEP = DISPATCH_CHUNK / MAX_E_LOCAL;
     const int e = tid % MAX_E_LOCAL;
     int pre = 0, tot = 0;
 #pragma unroll 4
@@ -192,47 +203,40 @@ dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
     s_part[0][tid] = pre;
     s_part[1][tid] = tot;
   }
-  __syncthreads();
-  if (tid < e_local) {
-    int pre = 0, tot = 0;
-#pragma unroll
-    for (int j = 0; j < DISPATCH_CHUNK / MAX_E_LOCAL; ++j) {
-      pre += s_part[0][j * MAX_E_LOCAL + tid];
-      tot += s_part[1][j * MAX_E_LOCAL + tid];
-    }
-    s_pre[tid] = pre;
-    s_tot[tid] = tot;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int acc = 0;
-    for (int e = 0; e < e_local; ++e) {
-      s_base[e] = acc + s_pre[e];
-      if (blockIdx.x == 0) { counts[e] = s_tot[e]; offsets[e] = acc; }
-      acc += s_tot[e];
-    }
-    if (blockIdx.x == 0) offsets[e_local] = acc;
-  }
-
-  const int t = c0 + tid;
-  const bool valid = t < T;
-  int ids[TOP_K];
-  float ws[TOP_K];
-#pragma unroll
-  for (int k = 0; k < TOP_K; ++k) {
-    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
-    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
-  }
   const uint32_t m = valid ? local_mask(ids, offset, e_local) : 0u;
   for (int e = 0; e < e_local; ++e) {
     const uint64_t bal = __ballot((m >> e) & 1u);
     if (lane == 0) s_wtot[wave][e] = __popcll(bal);
   }
   __syncthreads();
-  if (tid < e_local) {
+  if (tid < MAX_E_LOCAL) {
+    // Lane e of wave 0: expert e's picks before this chunk and in total, the
+    // exclusive scan of the totals over experts (offsets[e]) by shuffles,
+    // and the waves' offsets inside this chunk.
+    const bool live = tid < e_local;
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int j = 0; j < CSTEP; ++j) {
+      pre += s_part[0][j * MAX_E_LOCAL + tid];
+      tot += s_part[1][j * MAX_E_LOCAL + tid];
+    }
+    if (!live) pre = tot = 0;
+    int inc = tot;
+#pragma unroll
+    for (int d = 1; d < MAX_E_LOCAL; d <<= 1) {
+      const int o = __shfl_up(inc, d);
+      if (tid >= d) inc += o;
+    }
+    const int excl = inc - tot;
+    s_base[tid] = excl + pre;
+    if (blockIdx.x == 0 && live) {
+      counts[tid] = tot;
+      offsets[tid] = excl;
+      if (tid == e_local - 1) offsets[e_local] = inc;
+    }
     int acc = 0;
 #pragma unroll
-    for (int w = 0; w < NWAVE; ++w) { s_woff[w][tid] = acc; acc += s_wtot[w][tid]; }
+    for (int w = 0; w < NWAVE; ++w) { s_woff[w][tid] = acc; acc += live ? s_wtot[w][tid] : 0; }
   }
   __syncthreads();
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
