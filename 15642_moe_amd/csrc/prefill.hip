@@ -157,18 +157,35 @@ struct ActStage {
     s_scl[b * G::NT + tid] = make_float2(sc * w0, sc * w1);
   }
   // K-block rows at abase_k = activations + K-block offset, scales at sbase_k.
+  // Only the first NI chunks per thread (routes 0 .. 8*NI*NT/64 - 1) move:
+  // an item whose routes fill NC < CT route tiles gathers no padding past
+  // them (the gather's address work, not its bytes, bounds a sparse item).
+  template <int NI = G::ACH>
   __device__ __forceinline__ void load(const uint8_t* abase_k, const float* sbase_k, const GatherAddr<CT, RW, NW>& ga,
                                        int tid) {
 #pragma unroll
-    for (int i = 0; i < G::ACH; ++i) load_chunk(i, abase_k, ga, tid);
+    for (int i = 0; i < NI; ++i) load_chunk(i, abase_k, ga, tid);
     load_scale(sbase_k, ga);
   }
+  template <int NI = G::ACH>
   __device__ __forceinline__ void store(uint8_t* s_act, float2* s_scl, int b, int tid, float w0, float w1) const {
 #pragma unroll
-    for (int i = 0; i < G::ACH; ++i) store_chunk(i, s_act, b, tid);
+    for (int i = 0; i < NI; ++i) store_chunk(i, s_act, b, tid);
     store_scale(s_scl, b, tid, w0, w1);
   }
 };
+
+// Chunks per thread that an item body with NC route tiles per wave must
+// stage: chunk i of every thread covers routes i*NT/8 .. (i+1)*NT/8 - 1, so
+// routes below 16*NC need i < 128*NC/NT.  Only when every wave owns the
+// same route tiles (RW == NW); otherwise waves with different NC share one
+// staging and all of it moves.
+template <int CT, int RW, int NW>
+constexpr int active_chunks(int nc) {
+  using G = TileGeom<CT, RW, NW>;
+  const int need = (128 * nc + G::NT - 1) / G::NT;
+  return (RW == NW && need < G::ACH) ? need : G::ACH;
+}
 
 // Per-step barrier: this wave's LDS stores are complete, then all waves meet.
 // Written as one statement so no VMEM wait is attached to it.
@@ -311,8 +328,14 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
   const int n_work = s_tp[e_local] * IB;
   const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
 
+  // Thread 0 takes the next item from the queue as soon as the current
+  // item's K loop is done, so the atomic's round trip runs under the
+  // epilogue (taken any earlier, the claim would hold an item back from a
+  // workgroup that frees up first).
+  int claimed = 0;
+  if (tid == 0) claimed = atomicAdd(&queue[q], 1);
   for (;;) {
-    if (tid == 0) s_item = seg_lo + atomicAdd(&queue[q], 1);
+    if (tid == 0) s_item = seg_lo + claimed;
     __syncthreads();
     const int L = __builtin_amdgcn_readfirstlane(s_item);
     if (L >= seg_hi) break;
@@ -344,6 +367,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     // loop and epilogue), so no accumulator crosses between them.
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
       constexpr int NC = decltype(nct)::value;
+      constexpr int NI = active_chunks<CT, RW, NW>(NC);
       v8i wf[WS][WT];
       auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W13_KB_BYTES + t * TILE_BYTES, lane); };
       v4f acc[WT][CW];
@@ -362,9 +386,9 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
       for (int a0 = 0; a0 < AS; ++a0)
-        st[a0].load(hidden + (size_t)a0 * BLK, hscale + (size_t)a0 * T, ga, tid);
-      st[0].store(s_act, s_scl, 0, tid, lane_value(wsg_l, 0), lane_value(wsu_l, 0));
-      st[0].load(hidden + (size_t)AS * BLK, hscale + (size_t)AS * T, ga, tid);
+        st[a0].template load<NI>(hidden + (size_t)a0 * BLK, hscale + (size_t)a0 * T, ga, tid);
+      st[0].template store<NI>(s_act, s_scl, 0, tid, lane_value(wsg_l, 0), lane_value(wsu_l, 0));
+      st[0].template load<NI>(hidden + (size_t)AS * BLK, hscale + (size_t)AS * T, ga, tid);
 
 #pragma unroll 1
       for (int kb0 = 0; kb0 < HB; kb0 += 4) {
@@ -384,12 +408,14 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
           if constexpr (NC > 0)
             pipe.template step<NC>(s, acc, wf[s % WS], afl + (s & 1) * TILE_BYTES, afh + (s & 1) * TILE_BYTES, asp,
                                    kb == 0);
-          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, lane_value(wsg_l, k1), lane_value(wsu_l, k1));
+          st[(s + 1) % AS].template store<NI>(s_act, s_scl, (s + 1) & 1, tid, lane_value(wsg_l, k1),
+                                              lane_value(wsu_l, k1));
           __builtin_amdgcn_sched_barrier(0);  // the set's registers are free only after its stores
-          st[(s + 1) % AS].load(hidden + (size_t)ka * BLK, hscale + (size_t)ka * T, ga, tid);
+          st[(s + 1) % AS].template load<NI>(hidden + (size_t)ka * BLK, hscale + (size_t)ka * T, ga, tid);
         }
       }
       if constexpr (NC > 0) pipe.template drain<NC>(acc);
+      if (tid == 0) claimed = atomicAdd(&queue[q], 1);
 
       // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
 #pragma unroll
@@ -458,6 +484,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * 2 * TILE_BYTES];
   __shared__ float2 s_scl[2 * G::NT];
   __shared__ uint32_t s_rowoff[BM], s_soff[BM];
+  __shared__ float s_rw[BM];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -470,8 +497,14 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   const int n_work = s_tp[e_local] * NHP;
   const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
 
+  // Thread 0 takes the next item from the queue as soon as the current
+  // item's K loop is done, so the atomic's round trip runs under the
+  // epilogue (taken any earlier, the claim would hold an item back from a
+  // workgroup that frees up first).
+  int claimed = 0;
+  if (tid == 0) claimed = atomicAdd(&queue[q], 1);
   for (;;) {
-    if (tid == 0) s_item = seg_lo + atomicAdd(&queue[q], 1);
+    if (tid == 0) s_item = seg_lo + claimed;
     __syncthreads();
     const int L = __builtin_amdgcn_readfirstlane(s_item);
     if (L >= seg_hi) break;
@@ -480,6 +513,9 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const int m0 = mt * BM;
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
+    // Route tid's weight is read now and parked in LDS before the K loop,
+    // so the epilogue's multiply waits on no global load.
+    const float rw_mine = route_weight[rb + (tid < rows ? tid : 0)];
     for (int r = tid; r < BM; r += G::NT) {
       const int rr = rb + (r < rows ? r : 0);
       s_rowoff[r] = (uint32_t)rr * I;
@@ -501,6 +537,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
       constexpr int NC = decltype(nct)::value;
+      constexpr int NI = active_chunks<CT, RW, NW>(NC);
       v8i wf[WS][WT];
       auto wtile = [&](int kb, int t) { return load_tile_frag(wp + (size_t)kb * W2_KB_BYTES + t * TILE_BYTES, lane); };
       v4f acc[WT][CW];
@@ -516,9 +553,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 #pragma unroll
         for (int t = 0; t < WT; ++t) wf[w0][t] = wtile(w0, t);
 #pragma unroll
-      for (int a0 = 0; a0 < AS; ++a0) st[a0].load(Cq + (size_t)a0 * BLK, Cs + a0, ga, tid);
-      st[0].store(s_act, s_scl, 0, tid, lane_value(ws_l, 0), lane_value(ws_l, IB));
-      st[0].load(Cq + (size_t)AS * BLK, Cs + AS, ga, tid);
+      for (int a0 = 0; a0 < AS; ++a0) st[a0].template load<NI>(Cq + (size_t)a0 * BLK, Cs + a0, ga, tid);
+      st[0].template store<NI>(s_act, s_scl, 0, tid, lane_value(ws_l, 0), lane_value(ws_l, IB));
+      st[0].template load<NI>(Cq + (size_t)AS * BLK, Cs + AS, ga, tid);
+      if (tid < BM) s_rw[tid] = rw_mine;  // read after the K loop's barriers
 
 #pragma unroll 1
       for (int kb0 = 0; kb0 < IB; kb0 += 4) {
@@ -535,18 +573,20 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
           if constexpr (NC > 0)
             pipe.template step<NC>(s, acc, wf[s % WS], afl + (s & 1) * TILE_BYTES, afh + (s & 1) * TILE_BYTES, asp,
                                    kb == 0);
-          st[(s + 1) % AS].store(s_act, s_scl, (s + 1) & 1, tid, lane_value(ws_l, k1), lane_value(ws_l, IB + k1));
+          st[(s + 1) % AS].template store<NI>(s_act, s_scl, (s + 1) & 1, tid, lane_value(ws_l, k1),
+                                              lane_value(ws_l, IB + k1));
           __builtin_amdgcn_sched_barrier(0);
-          st[(s + 1) % AS].load(Cq + (size_t)ka * BLK, Cs + ka, ga, tid);
+          st[(s + 1) % AS].template load<NI>(Cq + (size_t)ka * BLK, Cs + ka, ga, tid);
         }
       }
       if constexpr (NC > 0) pipe.template drain<NC>(acc);
+      if (tid == 0) claimed = atomicAdd(&queue[q], 1);
 
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
         const int row = (wc * CW + cc) * 16 + (lane & 15);
         if (row < rows) {
-          const float rw = route_weight[rb + row];
+          const float rw = s_rw[row];
           float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
 #pragma unroll
           for (int t = 0; t < WT; ++t) {
