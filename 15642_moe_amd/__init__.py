@@ -11,11 +11,11 @@ The package directory name starts with a digit, so import it with
 
 from . import geometry  # noqa: F401
 
-__all__ = ["geometry", "ops", "moe_layer", "inputs", "capi"]
+__all__ = ["geometry", "ops", "moe_layer", "inputs", "capi", "checkpoint"]
 
 
 def __getattr__(name):
-    if name in ("ops", "moe_layer", "inputs", "capi"):
+    if name in ("ops", "moe_layer", "inputs", "capi", "checkpoint"):
         import importlib
 
         return importlib.import_module(f"{__name__}.{name}")

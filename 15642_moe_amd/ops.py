@@ -49,16 +49,26 @@ def _require_device(name: str, t: torch.Tensor, device: torch.device | None = No
 
 
 # --------------------------------------------------------------------------- packs
-def pack_w13(W13: torch.Tensor) -> torch.Tensor:
+def _check_out(out: torch.Tensor | None, shape: tuple, like: torch.Tensor, name: str) -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=torch.int32, device=like.device)
+    _check(out.dtype == torch.int32 and tuple(out.shape) == shape and out.is_contiguous(),
+           f"{name} out must be int32 {list(shape)} contiguous")
+    _require_device(f"{name} out", out, like.device)
+    return out
+
+
+def pack_w13(W13: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """W13 e4m3 [E_local, 4096, 7168] -> int32 packed MFMA operand tiles
-    (kernels/moe.cu:700-720)."""
+    (kernels/moe.cu:700-720).  `out` (optional) receives them in place, e.g.
+    one expert's slot ``packed[e:e+1]`` of a larger packed buffer."""
     _require_device("W13", W13)
     _check(W13.dim() == 3, "W13 must be [E_local, 4096, 7168]")
     _check(W13.element_size() == 1, "W13 must be an FP8 tensor")
     _check(W13.is_contiguous(), "W13 must be contiguous")
     E = int(W13.size(0))
     _check(W13.size(1) == 2 * I_DIM and W13.size(2) == H, "W13 must be [E_local, 4096, 7168]")
-    out = torch.empty((E, *W13_PACKED_SHAPE), dtype=torch.int32, device=W13.device)
+    out = _check_out(out, (E, *W13_PACKED_SHAPE), W13, "pack_w13")
     if E == 0:
         return out
     with torch.cuda.device(W13.device):
@@ -66,16 +76,16 @@ def pack_w13(W13: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def pack_w2(W2: torch.Tensor) -> torch.Tensor:
+def pack_w2(W2: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """W2 e4m3 [E_local, 7168, 2048] -> int32 packed MFMA operand tiles
-    (kernels/moe.cu:722-742)."""
+    (kernels/moe.cu:722-742); `out` as for pack_w13."""
     _require_device("W2", W2)
     _check(W2.dim() == 3, "W2 must be [E_local, 7168, 2048]")
     _check(W2.element_size() == 1, "W2 must be an FP8 tensor")
     _check(W2.is_contiguous(), "W2 must be contiguous")
     E = int(W2.size(0))
     _check(W2.size(1) == H and W2.size(2) == I_DIM, "W2 must be [E_local, 7168, 2048]")
-    out = torch.empty((E, *W2_PACKED_SHAPE), dtype=torch.int32, device=W2.device)
+    out = _check_out(out, (E, *W2_PACKED_SHAPE), W2, "pack_w2")
     if E == 0:
         return out
     with torch.cuda.device(W2.device):
