@@ -485,6 +485,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   __shared__ float2 s_scl[2 * G::NT];
   __shared__ uint32_t s_rowoff[BM], s_soff[BM];
   __shared__ float s_rw[BM];
+  // Per-wave transpose of one route tile's Y (16 routes x 32 floats, rows
+  // padded to 36 floats) when a wave owns two row tiles (WT == 2).
+  constexpr int YT_STRIDE = 36;
+  __shared__ __attribute__((aligned(16))) float s_yt[WT == 2 ? NW : 1][16 * YT_STRIDE];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -582,16 +586,47 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       if constexpr (NC > 0) pipe.template drain<NC>(acc);
       if (tid == 0) claimed = atomicAdd(&queue[q], 1);
 
+      if constexpr (WT == 2) {
+        // A lane holds 4 columns of each of its two row tiles for one route;
+        // through this wave's LDS slot, each store instruction instead writes
+        // 8 routes' whole 128-byte segments (8 full lines, not 16 half lines).
+        // The lane index passes through an empty asm so that these address
+        // terms are formed here, not hoisted out of the item loop to occupy
+        // registers across the K loop.
+        int ln = lane;
+        __asm__ volatile("" : "+v"(ln));
+        float* yt = s_yt[w];
+        const int rr = ln >> 3, ch = ln & 7;
 #pragma unroll
-      for (int cc = 0; cc < NC; ++cc) {
-        const int row = (wc * CW + cc) * 16 + (lane & 15);
-        if (row < rows) {
-          const float rw = s_rw[row];
-          float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+        for (int cc = 0; cc < NC; ++cc) {
+          const int r0 = (wc * CW + cc) * 16;
+          const float rw = s_rw[r0 + (ln & 15)];
 #pragma unroll
-          for (int t = 0; t < WT; ++t) {
+          for (int t = 0; t < 2; ++t) {
             const v4f y = acc[t][cc] * rw;
-            *reinterpret_cast<float4*>(yrow + 16 * t) = make_float4(y[0], y[1], y[2], y[3]);
+            *reinterpret_cast<float4*>(yt + (ln & 15) * YT_STRIDE + 16 * t + 4 * (ln >> 4)) =
+                make_float4(y[0], y[1], y[2], y[3]);
+          }
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int r = r0 + rr + 8 * h;
+            const float4 v = *reinterpret_cast<const float4*>(yt + (rr + 8 * h) * YT_STRIDE + 4 * ch);
+            if (r < rows) *reinterpret_cast<float4*>(Y + (size_t)(rb + r) * H + hb * BLK + 16 * t0 + 4 * ch) = v;
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one route tile at a time: few registers live
+        }
+      } else {
+#pragma unroll
+        for (int cc = 0; cc < NC; ++cc) {
+          const int row = (wc * CW + cc) * 16 + (lane & 15);
+          if (row < rows) {
+            const float rw = s_rw[row];
+            float* yrow = Y + (size_t)(rb + row) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+#pragma unroll
+            for (int t = 0; t < WT; ++t) {
+              const v4f y = acc[t][cc] * rw;
+              *reinterpret_cast<float4*>(yrow + 16 * t) = make_float4(y[0], y[1], y[2], y[3]);
+            }
           }
         }
       }
