@@ -33,7 +33,11 @@ and DeepSeek's MLP is down(silu(gate(x)) * up(x)), so
     routing_bias            = e_score_correction_bias                    [256]
 
 for le = e - local_expert_offset.  The router weight feeds the input
-producer (ops.pack_router / ops.router_quant).
+producer (ops.pack_router / ops.router_quant).  Naming caution: the
+reference kernel calls GEMM1 rows [0, I) "gate" and rows [I, 2I) "up"
+(kernels/moe.cu:483-487, the scale blocks nb and nb+16), the opposite of
+the checkpoint's names for the same rows; the kernels here follow the
+reference's naming.
 
 Files are opened with safetensors' own reader (no pickle); nothing in a
 checkpoint is executed.
