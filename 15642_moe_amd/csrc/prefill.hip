@@ -693,10 +693,8 @@ hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p,
     case TILE_64x256:
       return run_stage2_tile<4, 4, 4, 2, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
                                          max_routes, queue, stream);
-    case TILE_128x256:
-      return run_stage2_tile<8, 8, 2, 2, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                         max_routes, queue, stream);
-    default:
+    default:  // from 65 expected routes up: 192-route tiles (fewer, fuller items than 128-route
+              // tiles; measured faster on skewed routing and equal on uniform)
       return run_stage2_tile<12, 8, 2, 1, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
                                           max_routes, queue, stream);
   }
