@@ -635,13 +635,16 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   }
 }
 
-// Tile shape for a launch from the expected routes per local expert
-// (T * 8 / 256 under uniform routing; skewed routing only adds tiles).
-enum TileShape { TILE_64x256, TILE_128x256, TILE_192x256 };
-TileShape tile_shape(int T) {
-  const int expected = T / 32;
-  return expected <= 64 ? TILE_64x256 : (expected <= 128 ? TILE_128x256 : TILE_192x256);
-}
+// GEMM1 tile for a launch from the expected routes per local expert
+// (T * 8 / 256 under uniform routing; skewed routing only adds tiles):
+// 128-route tiles up to 128 expected routes, 192-route tiles above.  GEMM2
+// always takes 192-route tiles.  Measured on MI355X: the 64-route shape
+// (4 row groups x 2 route groups) was slower at every T tried (T=512 GEMM1
+// 174 vs 158 us, T=2048 231 vs 173 us), 192-route GEMM1 tiles lost to
+// 128-route ones at 128 expected routes (uniform T=4096 260 vs 235 us), and
+// 192-route GEMM2 tiles won on skewed routing (406 vs 474 us) and tied on
+// uniform.
+bool stage1_wide_tiles(int T) { return T / 32 > 128; }
 
 template <int CT, int RW, int WS, int AS, int NW>
 hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
@@ -673,31 +676,19 @@ hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local, int max_routes,
                          int32_t* queue, hipStream_t stream) {
-  switch (tile_shape(T)) {
-    case TILE_64x256:
-      return run_stage1_tile<4, 4, 4, 2, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
-                                         T, e_local, max_routes, queue, stream);
-    case TILE_128x256:
-      return run_stage1_tile<8, 8, 2, 2, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
-                                         T, e_local, max_routes, queue, stream);
-    default:
-      return run_stage1_tile<12, 8, 2, 1, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
-                                          Cs, T, e_local, max_routes, queue, stream);
-  }
+  if (!stage1_wide_tiles(T))
+    return run_stage1_tile<8, 8, 2, 2, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                       T, e_local, max_routes, queue, stream);
+  return run_stage1_tile<12, 8, 2, 1, 8>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
+                                        T, e_local, max_routes, queue, stream);
 }
 
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
-                         const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y, int T,
-                         int e_local, int max_routes, int32_t* queue, hipStream_t stream) {
-  switch (tile_shape(T)) {
-    case TILE_64x256:
-      return run_stage2_tile<4, 4, 4, 2, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                         max_routes, queue, stream);
-    default:  // from 65 expected routes up: 192-route tiles (fewer, fuller items than 128-route
-              // tiles; measured faster on skewed routing and equal on uniform)
-      return run_stage2_tile<12, 8, 2, 1, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local,
-                                          max_routes, queue, stream);
-  }
+                         const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
+                         int /*T: one tile shape for every T*/, int e_local, int max_routes, int32_t* queue,
+                         hipStream_t stream) {
+  return run_stage2_tile<12, 8, 2, 1, 8>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y, e_local, max_routes,
+                                        queue, stream);
 }
 
 }  // namespace moe
