@@ -189,6 +189,30 @@ def test_forward_full_size_sampled(ops, inputs_mod, cuda, packed_cache, idx):
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
 
 
+@pytest.mark.parametrize("T", [128, 129, 4160])
+def test_forward_path_boundaries(ops, inputs_mod, cuda, packed_cache, T):
+    """Either side of the decode / prefill switch (T = 128 | 129) and just
+    past the GEMM1 tile switch (T/32 > 128: 192-route tiles), BASELINE
+    distributions; routing against the oracle, output on sampled tokens."""
+    print(f"[forward] boundary T={T}", flush=True)
+    packed_cache.clear()
+    torch.cuda.empty_cache()
+    cfg = inputs_mod.Config(100 + T, f"boundary_T{T}", T, 0, False, 0x15642100 + T)
+    inp = inputs_mod.make_config_inputs(cfg, device=cuda)
+    p13, p2 = ops.pack_w13(inp["gemm1_weights"]), ops.pack_w2(inp["gemm2_weights"])
+    out, ws = _forward(ops, inp, p13, p2)
+    torch.cuda.synchronize()
+    ids = ops.workspace_views(ws, T, 32)["topk_ids"].cpu().numpy()
+    inp_cpu = _cpu(inp)
+    want = routing.route(inp_cpu["routing_logits"].to(torch.float32).numpy(),
+                         inp_cpu["routing_bias"].to(torch.float32).numpy(), float(inp["routed_scaling_factor"]))
+    assert np.array_equal(ids, want["ids"])
+    toks = _sample_tokens(ids, 0) if T > 1024 else None
+    _check_against_models(f"boundary T={T}", out, inp_cpu, token_subset=toks)
+    out2, _ = _forward(ops, inp, p13, p2)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
 def test_forward_rsf_scaling(ops, inputs_mod, cuda, packed_cache):
     """Output is linear in routed_scaling_factor (power-of-two factor: exact
     in fp32 before the bf16 rounding, so the bits scale exactly)."""
