@@ -144,6 +144,34 @@ __device__ __forceinline__ uint32_t chunk_token_mask(const int32_t* __restrict__
   return t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
 }
 
+// Writes token t's local routes (its bit mask m over local experts): route
+// r = s_base[e] + wave_off[e] + (lanes below this one in the wave that also
+// picked e), so slots follow token order within each expert; token_route
+// lists the routes in ascending expert order, -1 after the last.
+__device__ __forceinline__ void place_token(uint32_t m, const int* ids, const float* ws, int t, bool valid, int offset,
+                                            int e_local, const int* s_base, const int* wave_off, int lane,
+                                            int32_t* __restrict__ route_token, float* __restrict__ route_weight,
+                                            int32_t* __restrict__ token_route) {
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int j = 0;
+  for (int e = 0; e < e_local; ++e) {
+    const uint64_t bal = __ballot((m >> e) & 1u);
+    if ((m >> e) & 1u) {
+      const int r = s_base[e] + wave_off[e] + __popcll(bal & lt_mask);
+      float wsel = 0.0f;
+#pragma unroll
+      for (int k = 0; k < TOP_K; ++k)
+        if (ids[k] - offset == e) wsel = ws[k];
+      route_token[r] = t;
+      route_weight[r] = wsel;
+      token_route[(size_t)t * TOP_K + j] = r;
+      ++j;
+    }
+  }
+  if (valid)
+    for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
+}
+
 __global__ void __launch_bounds__(DISPATCH_CHUNK)
 dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T, int e_local, int offset,
                       int32_t* __restrict__ chunk_counts, int32_t* __restrict__ queue) {
@@ -239,24 +267,8 @@ dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
     for (int w = 0; w < NWAVE; ++w) { s_woff[w][tid] = acc; acc += live ? s_wtot[w][tid] : 0; }
   }
   __syncthreads();
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int j = 0;
-  for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
-    if ((m >> e) & 1u) {
-      const int r = s_base[e] + s_woff[wave][e] + __popcll(bal & lt_mask);
-      float wsel = 0.0f;
-#pragma unroll
-      for (int k = 0; k < TOP_K; ++k)
-        if (ids[k] - offset == e) wsel = ws[k];
-      route_token[r] = t;
-      route_weight[r] = wsel;
-      token_route[(size_t)t * TOP_K + j] = r;
-      ++j;
-    }
-  }
-  if (valid)
-    for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
+  place_token(m, ids, ws, t, valid, offset, e_local, s_base, s_woff[wave], lane, route_token, route_weight,
+              token_route);
 }
 
 // Up to DISPATCH_SMALL_T tokens (one chunk) the whole dispatch is one
@@ -318,24 +330,8 @@ dispatch_small_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
     }
   }
   __syncthreads();
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int j = 0;
-  for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
-    if ((m >> e) & 1u) {
-      const int r = s_base[e] + s_woff[wave][e] + __popcll(bal & lt_mask);
-      float wsel = 0.0f;
-#pragma unroll
-      for (int k = 0; k < TOP_K; ++k)
-        if (ids[k] - offset == e) wsel = ws[k];
-      route_token[r] = t;
-      route_weight[r] = wsel;
-      token_route[(size_t)t * TOP_K + j] = r;
-      ++j;
-    }
-  }
-  if (valid)
-    for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
+  place_token(m, ids, ws, t, valid, offset, e_local, s_base, s_woff[wave], lane, route_token, route_weight,
+              token_route);
 }
 
 // out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ).
