@@ -48,10 +48,14 @@ __device__ __forceinline__ void load_tile_table(const int32_t* __restrict__ coun
 // XCD fetches each weight K-block into that XCD's L2 once for all of them
 // (an expert's route tiles also re-read their activations once per weight
 // block, but a route tile's K-block is smaller than a weight block's).
+// The expert is found by one LDS read per lane and a ballot (lane l tests
+// expert l), not a scan of dependent reads: L < s_tp[e_local] * nblk is a
+// valid work, so exactly one expert's range holds it.
 __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const int* s_tp, int& e, int& blk,
                                             int& mt) {
-  e = 0;
-  while (e + 1 < e_local && s_tp[e + 1] * nblk <= L) ++e;
+  const int l = threadIdx.x & 63, li = l < e_local ? l : 0;  // every read inside s_tp[0 .. e_local]
+  const bool mine = l < e_local && s_tp[li] * nblk <= L && L < s_tp[li + 1] * nblk;
+  e = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(mine)));
   const int nt = s_tp[e + 1] - s_tp[e];  // >= 1: L lies inside expert e's works
   const int local = L - s_tp[e] * nblk;
   blk = local / nt;
