@@ -344,6 +344,10 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     const int m0 = mt * BM;
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
+    // Gate / up weight-block scales of K-block k in lane k, read before the
+    // row table so their latency overlaps its loads.
+    const float wsg_l = w13s[(size_t)(e * G1B + nb) * HB + min(lane, HB - 1)];
+    const float wsu_l = w13s[(size_t)(e * G1B + IB + nb) * HB + min(lane, HB - 1)];
     for (int r = tid; r < BM; r += G::NT) {
       const int tok = route_token[rb + (r < rows ? r : 0)];
       s_rowoff[r] = (uint32_t)tok * H;
@@ -360,9 +364,6 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     // Route tiles of this wave that hold routes (0 for route groups past the tile's routes).
     const int ncc = __builtin_amdgcn_readfirstlane(min(CW, max(0, (rows - wc * CW * 16 + 15) >> 4)));
     const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(wr * WT) * TILE_BYTES;
-    // Gate / up weight-block scales of K-block k in lane k.
-    const float wsg_l = w13s[(size_t)(e * G1B + nb) * HB + min(lane, HB - 1)];
-    const float wsu_l = w13s[(size_t)(e * G1B + IB + nb) * HB + min(lane, HB - 1)];
     // One instantiation of the item body per route-tile count (prologue, K
     // loop and epilogue), so no accumulator crosses between them.
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
@@ -518,8 +519,11 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
     // Route tid's weight is read now and parked in LDS before the K loop,
-    // so the epilogue's multiply waits on no global load.
+    // so the epilogue's multiply waits on no global load; the weight-block
+    // scales (H block 2hp, K-block k in lane k; H block 2hp+1 in lane IB + k)
+    // are read here too, ahead of the row table.
     const float rw_mine = route_weight[rb + (tid < rows ? tid : 0)];
+    const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
     for (int r = tid; r < BM; r += G::NT) {
       const int rr = rb + (r < rows ? r : 0);
       s_rowoff[r] = (uint32_t)rr * I;
@@ -537,8 +541,6 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     // scale pair component (g0 >> 3) is this wave's H block
     const float* ascl = reinterpret_cast<const float*>(s_scl + wc * CW * 16 + (lane & 15)) + (g0 >> 3);
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
-    // Scales of H block 2hp, K-block k in lane k; of H block 2hp+1 in lane IB + k.
-    const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
     with_tile_count<TileQ<CW>::Q, CW>(ncc, [&](auto nct) {
       constexpr int NC = decltype(nct)::value;
       constexpr int NI = active_chunks<CT, RW, NW>(NC);
