@@ -418,7 +418,12 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
       if constexpr (NC > 0) pipe.template drain<NC>(acc);
       if (tid == 0) claimed = atomicAdd(&queue[q], 1);
 
-      // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators.
+      // SwiGLU (silu on the up half, rows I..2I-1) into the gate accumulators,
+      // and below the requant, with hardware reciprocals (v_rcp_f32, ~1 ulp)
+      // instead of IEEE divisions: the epilogue runs while the CU's MFMAs
+      // idle, and its divisions were ~20% of its VALU work.  The exponential
+      // is already the hardware one, so the result stays within the same
+      // few-ulp distance of the oracle's exact-division model.
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
 #pragma unroll
@@ -426,7 +431,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const float g = acc[2 * jj][cc][v], u = acc[2 * jj + 1][cc][v];
-            acc[2 * jj][cc][v] = (u / (1.0f + __expf(-u))) * g;
+            acc[2 * jj][cc][v] = (u * __builtin_amdgcn_rcpf(1.0f + __expf(-u))) * g;
           }
       }
       // Per-route amax over this wave's I columns, then over the RW row groups.
@@ -450,12 +455,13 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 #pragma unroll
           for (int r2 = 1; r2 < RW; ++r2) am = fmaxf(am, s_red[r2][row]);
           const float sc = fmaxf(am / E4M3_MAX, 1.0e-8f);
+          const float isc = __builtin_amdgcn_rcpf(sc);
           uint8_t* crow = Cq + (size_t)(rb + row) * I + nb * BLK + 4 * (lane >> 4);
 #pragma unroll
           for (int jj = 0; jj < NP; ++jj) {
             float q[4];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(acc[2 * jj][cc][v] / sc, -E4M3_MAX), E4M3_MAX);
+            for (int v = 0; v < 4; ++v) q[v] = fminf(fmaxf(acc[2 * jj][cc][v] * isc, -E4M3_MAX), E4M3_MAX);
             const uint32_t packed = cvt2_e4m3(q[0], q[1]) | (cvt2_e4m3(q[2], q[3]) << 16);
             *reinterpret_cast<uint32_t*>(crow + 16 * (wr * NP + jj)) = packed;
           }
