@@ -304,3 +304,21 @@ def test_forward_fewer_local_experts(ops, cuda):
     inp["local_expert_offset"] = 64
     out = layer.run_custom(ops, **inp)
     _check_against_models("E_local=8", out, _cpu(inp))
+
+
+@pytest.mark.parametrize("T", [128, 640])
+def test_forward_every_token_on_the_same_experts(ops, cuda, T):
+    """Every token picks experts 0..7: eight local experts hold T routes each
+    (the decode path's largest route count per expert at T=128, and
+    several full route tiles per expert on the prefill path at T=640)."""
+    from conftest import pkg
+
+    layer = pkg("moe_layer")
+    inp = layer.build_moe_inputs(T=T, device="cuda", seed=11)
+    logits = torch.full((T, 256), -10.0, device="cuda")
+    logits[:, :8] = 10.0 + torch.rand(T, 8, device="cuda")
+    inp["routing_logits"] = logits
+    print(f"[forward] all tokens on experts 0..7, T={T}", flush=True)
+    out = layer.run_custom(ops, **inp)
+    torch.cuda.synchronize()
+    _check_against_models(f"same experts T={T}", out, _cpu(inp))
