@@ -322,3 +322,26 @@ def test_forward_every_token_on_the_same_experts(ops, cuda, T):
     out = layer.run_custom(ops, **inp)
     torch.cuda.synchronize()
     _check_against_models(f"same experts T={T}", out, _cpu(inp))
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_forward_random_shapes(ops, cuda, case):
+    """Seeded random (T, local_expert_offset, E_local, routed_scaling_factor)
+    through the reference's own entry point, against both CPU models."""
+    from conftest import pkg
+
+    layer = pkg("moe_layer")
+    rng = np.random.default_rng(1000 + case)
+    T = int(rng.choice([1, 2, 33, 97, 128, 129, 300, 700]))
+    e_local = int(rng.integers(1, 33))
+    offset = int(rng.integers(-16, 256))
+    inp = layer.build_moe_inputs(T=T, device="cuda", seed=int(rng.integers(0, 2**31)))
+    for k in ("gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale"):
+        inp[k] = inp[k][:e_local].contiguous()
+    inp["local_expert_offset"] = offset
+    inp["routed_scaling_factor"] = float(rng.uniform(0.5, 3.0))
+    inp["routing_bias"] = torch.from_numpy((rng.standard_normal(256) * 0.1).astype(np.float32)).to("cuda")
+    print(f"[forward] random case {case}: T={T} E_local={e_local} offset={offset}", flush=True)
+    out = layer.run_custom(ops, **inp)
+    torch.cuda.synchronize()
+    _check_against_models(f"random case {case}", out, _cpu(inp))
