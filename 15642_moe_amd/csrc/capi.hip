@@ -226,7 +226,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
                        "stage1_decode_kernel launch"));
     MOE_TRY(mark(3));
     MOE_TRY(hip_status(moe::launch_stage2_decode(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts,
-                                                 offsets, route_weight, Y, e_local, st),
+                                                 offsets, route_weight, Y, e_local, T, st),
                        "stage2_decode_kernel launch"));
   } else {
     MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,

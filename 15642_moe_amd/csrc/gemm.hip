@@ -78,7 +78,7 @@ __device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice
 // with wave ballots (counts, offsets, its expert's tokens in token order);
 // items j == 0 publish their expert's route arrays, item (0, 0) the counts,
 // offsets and the -1 tails of token_route.
-template <int NR>
+template <int NR, int FR>
 __global__ void __launch_bounds__(64)
 stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
                      int offset, const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
@@ -153,17 +153,25 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
   const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(2 * pj) * TILE_BYTES;
   const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
   const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
-  for (int m0 = 0; m0 < my_cnt; m0 += BM) {
+  // FR 16-route fragments per pass over the weight tiles: an expert with
+  // more routes than one fragment streams its tiles once per FR fragments.
+  for (int m0 = 0; m0 < my_cnt; m0 += BM * FR) {
     __asm__ volatile("" ::: "memory");  // keep the weight prologue inside the loop
-    const int rows = min(BM, my_cnt - m0);
-    const int tok = s_tok[m0 + (col < rows ? col : 0)];  // padding columns reuse a real row
-    const uint32_t avoff = (uint32_t)tok * H + 32 * (lane >> 4), svoff = (uint32_t)tok * 4;
+    int rows[FR];
+    uint32_t avoff[FR], svoff[FR];
+#pragma unroll
+    for (int f = 0; f < FR; ++f) {
+      rows[f] = min(BM, my_cnt - m0 - f * BM);  // <= 0: a padding fragment (its loads reread route m0)
+      const int tok = s_tok[m0 + (col < rows[f] ? f * BM + col : 0)];  // padding columns reuse a real row
+      avoff[f] = (uint32_t)tok * H + 32 * (lane >> 4);
+      svoff[f] = (uint32_t)tok * 4;
+    }
     const uint32_t wvoff = (uint32_t)lane * 16;
-    // loads per K-block: 2 weight tiles x 2 halves, 2 activation halves, the
-    // activation scale and the two weight-block scales
-    constexpr int LPK = 4 * NPW + 5;
-    u32x4 wgl[NR][NPW], wgh[NR][NPW], wul[NR][NPW], wuh[NR][NPW], bl[NR], bh[NR];
-    float as[NR], sg[NR], su[NR];
+    // loads per K-block: 2 weight tiles x 2 halves, per fragment 2
+    // activation halves and the activation scale, the two weight-block scales
+    constexpr int LPK = 4 * NPW + 3 * FR + 2;
+    u32x4 wgl[NR][NPW], wgh[NR][NPW], wul[NR][NPW], wuh[NR][NPW], bl[NR][FR], bh[NR][FR];
+    float as[NR][FR], sg[NR], su[NR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W13_KB_BYTES;
 #pragma unroll
@@ -171,16 +179,21 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         gload2(wgl[sl][p], wgh[sl][p], wvoff, pw + 2 * p * TILE_BYTES);
         gload2(wul[sl][p], wuh[sl][p], wvoff, pw + (2 * p + 1) * TILE_BYTES);
       }
-      gload2_adj(bl[sl], bh[sl], avoff, hidden + (size_t)kb * BLK);
-      gload1(as[sl], svoff, hscale + (size_t)kb * T);
+#pragma unroll
+      for (int f = 0; f < FR; ++f) {
+        gload2_adj(bl[sl][f], bh[sl][f], avoff[f], hidden + (size_t)kb * BLK);
+        gload1(as[sl][f], svoff[f], hscale + (size_t)kb * T);
+      }
       gload1(sg[sl], 0u, wsg_p + kb);
       gload1(su[sl], 0u, wsu_p + kb);
     };
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
-    v4f accg[NPW], accu[NPW];
+    v4f accg[FR][NPW], accu[FR][NPW];
 #pragma unroll
-    for (int p = 0; p < NPW; ++p) { accg[p] = zero4; accu[p] = zero4; }
+    for (int f = 0; f < FR; ++f)
+#pragma unroll
+      for (int p = 0; p < NPW; ++p) { accg[f][p] = zero4; accu[f][p] = zero4; }
 #pragma unroll 1
     for (int kb0 = 0; kb0 < HB; kb0 += NR) {
 #pragma unroll
@@ -190,26 +203,35 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         wait_vm<LPK * (NR - 1)>();
 #pragma unroll
         for (int p = 0; p < NPW; ++p) __asm__ volatile("" : "+v"(wgl[sl][p]), "+v"(wgh[sl][p]), "+v"(wul[sl][p]), "+v"(wuh[sl][p]));
-        __asm__ volatile("" : "+v"(bl[sl]), "+v"(bh[sl]), "+v"(as[sl]), "+v"(sg[sl]), "+v"(su[sl]));
-        const v8i bq = frag(bl[sl], bh[sl]);
 #pragma unroll
-        for (int p = 0; p < NPW; ++p) {
-          accg[p] += mfma_16x16x128_fp8(frag(wgl[sl][p], wgh[sl][p]), bq, zero4) * (as[sl] * sg[sl]);
-          accu[p] += mfma_16x16x128_fp8(frag(wul[sl][p], wuh[sl][p]), bq, zero4) * (as[sl] * su[sl]);
+        for (int f = 0; f < FR; ++f) __asm__ volatile("" : "+v"(bl[sl][f]), "+v"(bh[sl][f]), "+v"(as[sl][f]));
+        __asm__ volatile("" : "+v"(sg[sl]), "+v"(su[sl]));
+#pragma unroll
+        for (int f = 0; f < FR; ++f) {
+          const v8i bq = frag(bl[sl][f], bh[sl][f]);
+#pragma unroll
+          for (int p = 0; p < NPW; ++p) {
+            accg[f][p] += mfma_16x16x128_fp8(frag(wgl[sl][p], wgh[sl][p]), bq, zero4) * (as[sl][f] * sg[sl]);
+            accu[f][p] += mfma_16x16x128_fp8(frag(wul[sl][p], wuh[sl][p]), bq, zero4) * (as[sl][f] * su[sl]);
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vm<0>();  // the dead tail loads land before the registers are reused
-    if (col < rows) {
 #pragma unroll
-      for (int p = 0; p < NPW; ++p) {
-        float4 c;
-        c.x = (accu[p][0] / (1.0f + __expf(-accu[p][0]))) * accg[p][0];
-        c.y = (accu[p][1] / (1.0f + __expf(-accu[p][1]))) * accg[p][1];
-        c.z = (accu[p][2] / (1.0f + __expf(-accu[p][2]))) * accg[p][2];
-        c.w = (accu[p][3] / (1.0f + __expf(-accu[p][3]))) * accg[p][3];
-        *reinterpret_cast<float4*>(Cf + (size_t)(my_off + m0 + col) * I + 16 * (j * NPW + p) + 4 * (lane >> 4)) = c;
+    for (int f = 0; f < FR; ++f) {
+      if (col < rows[f]) {
+#pragma unroll
+        for (int p = 0; p < NPW; ++p) {
+          float4 c;
+          c.x = (accu[f][p][0] / (1.0f + __expf(-accu[f][p][0]))) * accg[f][p][0];
+          c.y = (accu[f][p][1] / (1.0f + __expf(-accu[f][p][1]))) * accg[f][p][1];
+          c.z = (accu[f][p][2] / (1.0f + __expf(-accu[f][p][2]))) * accg[f][p][2];
+          c.w = (accu[f][p][3] / (1.0f + __expf(-accu[f][p][3]))) * accg[f][p][3];
+          *reinterpret_cast<float4*>(Cf + (size_t)(my_off + m0 + f * BM + col) * I + 16 * (j * NPW + p) +
+                                     4 * (lane >> 4)) = c;
+        }
       }
     }
   }
@@ -243,7 +265,7 @@ quant_kernel(const float* __restrict__ Cf, const int32_t* __restrict__ offsets, 
 
 // Stage 2, one wave per (expert e, 64-row H slice q): tiles 4*(q%2)..+3 of
 // the 128-row slab hb = q/2.
-template <int NR>
+template <int NR, int FR>
 __global__ void __launch_bounds__(64)
 stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
                      const float* __restrict__ w2s, const int32_t* __restrict__ counts,
@@ -264,27 +286,42 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
   const int col = lane & 15;
 
-  for (int m0 = 0; m0 < cnt; m0 += BM) {
+  // FR 16-route fragments per pass over the weight tiles (as in stage 1).
+  for (int m0 = 0; m0 < cnt; m0 += BM * FR) {
     __asm__ volatile("" ::: "memory");  // keep the weight prologue inside the loop
-    const int rows = min(BM, cnt - m0);
-    const int rb = off + m0;
-    const int r = rb + (col < rows ? col : 0);
-    const uint32_t avoff = (uint32_t)r * I + 32 * (lane >> 4), svoff = (uint32_t)r * IB * 4;
+    int rows[FR];
+    uint32_t avoff[FR], svoff[FR];
+#pragma unroll
+    for (int f = 0; f < FR; ++f) {
+      rows[f] = min(BM, cnt - m0 - f * BM);  // <= 0: a padding fragment (its loads reread route m0)
+      const int r = off + m0 + (col < rows[f] ? f * BM + col : 0);
+      avoff[f] = (uint32_t)r * I + 32 * (lane >> 4);
+      svoff[f] = (uint32_t)r * IB * 4;
+    }
     const uint32_t wvoff = (uint32_t)lane * 16;
-    constexpr int LPK = 12;  // 4 weight tiles x 2 halves, 2 activation halves, C scale, weight-block scale
-    u32x4 wl[NR][4], wh[NR][4], bl[NR], bh[NR];
-    float as[NR], sw[NR];
+    // 4 weight tiles x 2 halves, per fragment 2 activation halves and its C
+    // scale, the weight-block scale
+    constexpr int LPK = 9 + 3 * FR;
+    u32x4 wl[NR][4], wh[NR][4], bl[NR][FR], bh[NR][FR];
+    float as[NR][FR], sw[NR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W2_KB_BYTES;
 #pragma unroll
       for (int i = 0; i < 4; ++i) gload2(wl[sl][i], wh[sl][i], wvoff, pw + i * TILE_BYTES);
-      gload2_adj(bl[sl], bh[sl], avoff, Cq + (size_t)kb * BLK);
-      gload1(as[sl], svoff, Cs + kb);
+#pragma unroll
+      for (int f = 0; f < FR; ++f) {
+        gload2_adj(bl[sl][f], bh[sl][f], avoff[f], Cq + (size_t)kb * BLK);
+        gload1(as[sl][f], svoff[f], Cs + kb);
+      }
       gload1(sw[sl], 0u, ws_p + kb);
     };
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
-    v4f acc[4] = {zero4, zero4, zero4, zero4};
+    v4f acc[FR][4];
+#pragma unroll
+    for (int f = 0; f < FR; ++f)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[f][i] = zero4;
 #pragma unroll 1
     for (int kb0 = 0; kb0 < IB; kb0 += NR) {
 #pragma unroll
@@ -293,26 +330,34 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
         issue(min(kb + NR - 1, IB - 1), (sl + NR - 1) % NR);  // branch-free, clamped
         wait_vm<LPK * (NR - 1)>();
         __asm__ volatile("" : "+v"(wl[sl][0]), "+v"(wh[sl][0]), "+v"(wl[sl][1]), "+v"(wh[sl][1]), "+v"(wl[sl][2]),
-                         "+v"(wh[sl][2]), "+v"(wl[sl][3]), "+v"(wh[sl][3]), "+v"(bl[sl]), "+v"(bh[sl]), "+v"(as[sl]),
-                         "+v"(sw[sl]));
-        const float sc = as[sl] * sw[sl];
-        const v8i bq = frag(bl[sl], bh[sl]);
+                         "+v"(wh[sl][2]), "+v"(wl[sl][3]), "+v"(wh[sl][3]), "+v"(sw[sl]));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          __builtin_amdgcn_sched_barrier(0);
-          acc[i] += mfma_16x16x128_fp8(frag(wl[sl][i], wh[sl][i]), bq, zero4) * sc;
+        for (int f = 0; f < FR; ++f) __asm__ volatile("" : "+v"(bl[sl][f]), "+v"(bh[sl][f]), "+v"(as[sl][f]));
+#pragma unroll
+        for (int f = 0; f < FR; ++f) {
+          const float sc = as[sl][f] * sw[sl];
+          const v8i bq = frag(bl[sl][f], bh[sl][f]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            __builtin_amdgcn_sched_barrier(0);
+            acc[f][i] += mfma_16x16x128_fp8(frag(wl[sl][i], wh[sl][i]), bq, zero4) * sc;
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     wait_vm<0>();
-    if (col < rows) {
-      const float rw = route_weight[rb + col];
-      float* yrow = Y + (size_t)(rb + col) * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const v4f y = acc[i] * rw;
-        *reinterpret_cast<float4*>(yrow + 16 * i) = make_float4(y[0], y[1], y[2], y[3]);
+    for (int f = 0; f < FR; ++f) {
+      if (col < rows[f]) {
+        const int r = off + m0 + f * BM + col;
+        const float rw = route_weight[r];
+        float* yrow = Y + (size_t)r * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v4f y = acc[f][i] * rw;
+          *reinterpret_cast<float4*>(yrow + 16 * i) = make_float4(y[0], y[1], y[2], y[3]);
+        }
       }
     }
   }
@@ -351,9 +396,18 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
                                 hipStream_t stream) {
   if (T > DECODE_MAX_T) return hipErrorInvalidValue;
   const int grid = e_local * (I / 32);
-  stage1_decode_kernel<4><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale, w13p,
-                                                   w13_scale, counts, offsets, route_token, route_weight, token_route,
-                                                   Cf);
+  // Two fragments per weight pass once experts can hold more than 16
+  // routes often enough to matter; at T <= 64 one (its registers keep two
+  // waves per SIMD either way, but the second fragment's loads would be
+  // padding for nearly every item).
+  if (T > 64)
+    stage1_decode_kernel<4, 2><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
+                                                        w13p, w13_scale, counts, offsets, route_token, route_weight,
+                                                        token_route, Cf);
+  else
+    stage1_decode_kernel<4, 1><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
+                                                        w13p, w13_scale, counts, offsets, route_token, route_weight,
+                                                        token_route, Cf);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   const int R = T * (e_local < TOP_K ? e_local : TOP_K);
@@ -363,10 +417,14 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
 
 hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                                 const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
-                                int e_local, hipStream_t stream) {
+                                int e_local, int T, hipStream_t stream) {
   const int grid = e_local * (H / 64);
-  stage2_decode_kernel<4><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
-                                                   e_local);
+  if (T > 64)  // as stage 1: two fragments per weight pass
+    stage2_decode_kernel<4, 2><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
+                                                        e_local);
+  else
+    stage2_decode_kernel<4, 1><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
+                                                        e_local);
   return hipGetLastError();
 }
 

@@ -42,7 +42,7 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
                                 hipStream_t stream);
 hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                                 const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
-                                int e_local, hipStream_t stream);
+                                int e_local, int T, hipStream_t stream);
 
 // Producer of the forward's inputs (router logits + FP8 activations) from
 // bf16 hidden states; `partial` holds router_partial_bytes(T) (unused when 0).

@@ -97,7 +97,7 @@ HIPCC = shutil.which("hipcc") is not None or Path("/opt/rocm/bin/hipcc").exists(
 
 @pytest.mark.skipif(not HIPCC, reason="hipcc not available")
 def test_decode_asm_loads_keep_their_registers():
-    assert _check_source("gemm.hip", "decode_kernel") == 2
+    assert _check_source("gemm.hip", "decode_kernel") == 4  # stages 1 and 2, one or two fragments per pass
 
 
 @pytest.mark.skipif(not HIPCC, reason="hipcc not available")
