@@ -76,6 +76,9 @@ def routing_fixtures() -> dict:
 
 
 def _reference_run():
+    # The reference tree is read-only: importing it must not leave
+    # __pycache__ bytecode behind in it.
+    sys.dont_write_bytecode = True
     sys.path.insert(0, str(REFERENCE_DIR))
     ref = importlib.import_module("reference")
     return ref.run
