@@ -79,6 +79,42 @@ def _check_against_models(tag, out, inp_cpu, token_subset=None, ws_views=None):
     return km
 
 
+class _InterStats:
+    """Running comparison of stage-1 / stage-2 intermediates with the model."""
+
+    def __init__(self):
+        self.n_bytes = self.n_diff = self.n_bad = 0
+        self.worst_cs = self.worst_y = 0.0
+
+    def add(self, cq, cs, y_gpu, rw, cq_m, cs_m, c_m, w2b, s2):
+        """One expert's routes (or a chunk of them): GPU Cq/Cs/Y against the
+        model's Cq_m/Cs_m/c_m (stage 1), and stage 2 of the model fed the
+        GPU's own C against the GPU's Y."""
+        table = moe_cpu.E4M3_TABLE
+        self.worst_cs = max(self.worst_cs, float(np.max(np.abs(cs - cs_m) / cs_m)))
+        self.n_bytes += cq.size
+        self.n_diff += int(np.count_nonzero(cq != cq_m))
+        deq_g = (table[cq].reshape(-1, 16, 128) * cs[:, :, None]).reshape(cq.shape)
+        deq_m = (table[cq_m].reshape(-1, 16, 128) * cs_m[:, :, None]).reshape(cq.shape)
+        slack = np.abs(c_m) * 2.0 ** -3 + np.repeat(cs_m, 128, axis=1) * (2.0 ** -8 + 448 * 1e-4)
+        self.n_bad += int(np.count_nonzero(np.abs(deq_g - deq_m) > slack))
+        O = moe_cpu.stage2_model(cq, cs, w2b, s2)
+        M = moe_cpu.stage2_model(cq & 0x7F, cs, w2b & 0x7F, s2)  # sum of |c*w| * scales
+        y_ref = (O * rw[:, None]).astype(np.float64)
+        bound = (MFMA_REL_BOUND * M * np.abs(rw[:, None]) + 1e-6 * np.abs(y_ref)).astype(np.float64)
+        y_gpu = y_gpu.astype(np.float64)
+        self.worst_y = max(self.worst_y, float(np.max(np.abs(y_gpu - y_ref) / np.maximum(bound, 1e-30))))
+
+    def check(self, tag):
+        print(f"[parity] {tag} C: bytes={self.n_bytes} codes_differing={self.n_diff} "
+              f"({self.n_diff / max(self.n_bytes, 1):.2e}) beyond_one_step={self.n_bad} "
+              f"worst_C_scale_rel={self.worst_cs:.2e} stage2_isolated_Y/bound={self.worst_y:.2e}", flush=True)
+        assert self.worst_cs < 1e-4
+        assert self.n_bad == 0
+        assert self.n_diff <= max(8, self.n_bytes // 100)
+        assert self.worst_y <= 1.0, "GEMM2 on the GPU's own C differs from the model beyond the MFMA accuracy bound"
+
+
 def _check_intermediates(tag, v, km, inp_cpu):
     """Stage 1: C_scale to 1e-4 and dequantised C within one e4m3 step of the
     model (a code can move where c sits on a rounding boundary; near zero the
@@ -90,34 +126,37 @@ def _check_intermediates(tag, v, km, inp_cpu):
     offsets = v["offsets"].cpu().numpy()
     cq_all, cs_all = v["Cq"].cpu().numpy(), v["Cs"].cpu().numpy()
     y_all, rw_all = v["Y"], v["route_weight"].cpu().numpy()
-    table = moe_cpu.E4M3_TABLE
     s2 = inp_cpu["gemm2_weights_scale"].to(torch.float32).numpy()
-    n_bytes = n_diff = n_bad = 0
-    worst_cs = worst_y = 0.0
+    st = _InterStats()
     for le, ex in km["experts"].items():
         r0, r1 = int(offsets[le]), int(offsets[le + 1])
         assert r1 - r0 == len(ex["tokens"])
-        cq, cs = cq_all[r0:r1], cs_all[r0:r1]
-        worst_cs = max(worst_cs, float(np.max(np.abs(cs - ex["Cs"]) / ex["Cs"])))
-        n_bytes += cq.size
-        n_diff += int(np.count_nonzero(cq != ex["Cq"]))
-        deq_g = (table[cq].reshape(-1, 16, 128) * cs[:, :, None]).reshape(cq.shape)
-        deq_m = (table[ex["Cq"]].reshape(-1, 16, 128) * ex["Cs"][:, :, None]).reshape(cq.shape)
-        slack = np.abs(ex["c"]) * 2.0 ** -3 + np.repeat(ex["Cs"], 128, axis=1) * (2.0 ** -8 + 448 * 1e-4)
-        n_bad += int(np.count_nonzero(np.abs(deq_g - deq_m) > slack))
-        w2b = moe_cpu._u8(inp_cpu["gemm2_weights"][le])
-        O = moe_cpu.stage2_model(cq, cs, w2b, s2[le])
-        M = moe_cpu.stage2_model(cq & 0x7F, cs, w2b & 0x7F, s2[le])  # sum of |c*w| * scales
-        y_ref = (O * rw_all[r0:r1, None]).astype(np.float64)
-        bound = (MFMA_REL_BOUND * M * np.abs(rw_all[r0:r1, None]) + 1e-6 * np.abs(y_ref)).astype(np.float64)
-        y_gpu = y_all[r0:r1].cpu().numpy().astype(np.float64)
-        worst_y = max(worst_y, float(np.max(np.abs(y_gpu - y_ref) / np.maximum(bound, 1e-30))))
-    print(f"[parity] {tag} C: bytes={n_bytes} codes_differing={n_diff} ({n_diff / max(n_bytes, 1):.2e}) "
-          f"beyond_one_step={n_bad} worst_C_scale_rel={worst_cs:.2e} stage2_isolated_Y/bound={worst_y:.2e}", flush=True)
-    assert worst_cs < 1e-4
-    assert n_bad == 0
-    assert n_diff <= max(8, n_bytes // 100)
-    assert worst_y <= 1.0, "GEMM2 on the GPU's own C differs from the model beyond the MFMA accuracy bound"
+        st.add(cq_all[r0:r1], cs_all[r0:r1], y_all[r0:r1].cpu().numpy(), rw_all[r0:r1], ex["Cq"], ex["Cs"], ex["c"],
+               moe_cpu._u8(inp_cpu["gemm2_weights"][le]), s2[le])
+    st.check(tag)
+
+
+def _check_expert_routes(tag, v, inp_cpu, ids, le, chunk=512):
+    """Every route of local expert `le` (full-size configurations): the
+    dispatch lists its tokens in token order, and its C / C_scale / Y match
+    the kernel model, computed chunk by chunk to bound host memory."""
+    off = int(inp_cpu["local_expert_offset"])
+    offsets = v["offsets"].cpu().numpy()
+    r0, r1 = int(offsets[le]), int(offsets[le + 1])
+    toks = np.nonzero((ids == le + off).any(axis=1))[0]
+    assert r1 - r0 == len(toks) and len(toks) > 0
+    assert np.array_equal(v["route_token"][r0:r1].cpu().numpy(), toks)
+    a_bytes, a_scale = moe_cpu._u8(inp_cpu["hidden_states"]), moe_cpu._f32(inp_cpu["hidden_states_scale"])
+    w13b, s13 = moe_cpu._u8(inp_cpu["gemm1_weights"][le]), moe_cpu._f32(inp_cpu["gemm1_weights_scale"][le])
+    w2b, s2 = moe_cpu._u8(inp_cpu["gemm2_weights"][le]), moe_cpu._f32(inp_cpu["gemm2_weights_scale"][le])
+    st = _InterStats()
+    for c0 in range(0, len(toks), chunk):
+        tk = toks[c0:c0 + chunk]
+        rr = slice(r0 + c0, r0 + c0 + len(tk))
+        cq_m, cs_m, c_m = moe_cpu.stage1_model(a_bytes[tk], a_scale[:, tk].T.copy(), w13b, s13)
+        st.add(v["Cq"][rr].cpu().numpy(), v["Cs"][rr].cpu().numpy(), v["Y"][rr].cpu().numpy(),
+               v["route_weight"][rr].cpu().numpy(), cq_m, cs_m, c_m, w2b, s2)
+    st.check(f"{tag} expert {le} ({len(toks)} routes)")
 
 
 @pytest.mark.parametrize("idx", [0, 1, 2])
@@ -164,6 +203,23 @@ def _sample_tokens(ids, offset, n_each=16, seed=0):
     return sorted(set(int(t) for t in pick))
 
 
+def _fragment_boundary_tokens(ids, offset, e_local=32, step=16):
+    """Tokens holding the first and last route of every `step`-route fragment
+    of every local expert.  Dispatch slots follow token order, so the s-th
+    token (ascending) that picks expert e holds route slot s of e; 16 is the
+    MFMA operand width and every route tile of the GEMMs is a whole number of
+    such fragments, so each tile's first and last route is among these."""
+    pick = set()
+    for le in range(e_local):
+        tl = np.nonzero((ids == le + offset).any(axis=1))[0]
+        n = len(tl)
+        if n == 0:
+            continue
+        slots = set(range(0, n, step)) | set(range(step - 1, n, step)) | {n - 1}
+        pick.update(int(tl[s_]) for s_ in slots)
+    return pick
+
+
 @pytest.mark.parametrize("idx", [3, 4])
 def test_forward_full_size_sampled(ops, inputs_mod, cuda, packed_cache, idx):
     print(f"[forward] config {idx} (sampled tokens)", flush=True)
@@ -176,7 +232,7 @@ def test_forward_full_size_sampled(ops, inputs_mod, cuda, packed_cache, idx):
     ids = views["topk_ids"].cpu().numpy()
     assert np.array_equal(ids, fx["ids"])
     off = int(inp["local_expert_offset"])
-    toks = _sample_tokens(ids, off)
+    toks = sorted(set(_sample_tokens(ids, off)) | _fragment_boundary_tokens(ids, off))
     inp_cpu = _cpu(inp)
     _check_against_models(f"config{idx}[{len(toks)} tokens]", out, inp_cpu, token_subset=toks)
     # size-independent properties over the whole output
@@ -187,6 +243,28 @@ def test_forward_full_size_sampled(ops, inputs_mod, cuda, packed_cache, idx):
     assert torch.count_nonzero(outf[torch.from_numpy(local).to(cuda)].abs().sum(1) == 0).item() == 0
     out2, _ = _forward(ops, inp, p13, p2)
     assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
+def _largest_expert(idx):
+    fx = np.load(GOLDEN / f"routing_cfg{idx}.npz")
+    off = int(fx["offset"])
+    return int(np.argmax([(fx["ids"] == le + off).any(axis=1).sum() for le in range(32)]))
+
+
+@pytest.mark.parametrize("idx,le", [(3, "largest"), (4, 0), (4, 1), (4, 2), (4, 3)])
+def test_forward_full_size_expert_routes(ops, inputs_mod, cuda, packed_cache, idx, le):
+    """All routes of one expert at full size: the T=8192 expert with the most
+    routes, and each of the four experts that every token picks under the
+    skewed routing (4,096 routes, ~22 route tiles each)."""
+    le = _largest_expert(idx) if le == "largest" else le
+    print(f"[forward] config {idx}: every route of expert {le}", flush=True)
+    inp, p13, p2 = _prepared(idx, inputs_mod, ops, cuda, packed_cache)
+    out, ws = _forward(ops, inp, p13, p2)
+    torch.cuda.synchronize()
+    T = inp["hidden_states"].shape[0]
+    views = ops.workspace_views(ws, T, 32)
+    ids = views["topk_ids"].cpu().numpy()
+    _check_expert_routes(f"config{idx}", views, _cpu(inp), ids, le)
 
 
 @pytest.mark.parametrize("T", [128, 129, 4160])
@@ -254,6 +332,42 @@ def test_reference_builder_distributions(T, cuda):
     _check_against_models(f"builder T={T}", out, inp_cpu)
 
 
+@pytest.mark.parametrize("T", [2048, 4096, 8192, 16384])
+def test_reference_builder_distributions_large(T, cuda):
+    """The rest of the reference's T sweep (tests/test_moe.py:18, seed = T)
+    at its builder's distributions, through moe_layer.run_custom: routing
+    bit-exact against the oracle, the output on sampled tokens plus the first
+    and last route of every 16-route fragment of every expert against both
+    CPU models, and whole-output properties (zero rows exactly where a token
+    has no local route, finite, run-to-run bit identity)."""
+    from conftest import pkg
+
+    layer = pkg("moe_layer")
+    ops_mod = layer._load_custom_ops()
+    print(f"[forward] builder T={T}", flush=True)
+    inp = layer.build_moe_inputs(T=T, device="cuda", seed=T)
+    out = layer.run_custom(ops_mod, **inp)
+    torch.cuda.synchronize()
+    inp_cpu = _cpu(inp)
+    want = routing.route(inp_cpu["routing_logits"].to(torch.float32).numpy(),
+                         inp_cpu["routing_bias"].to(torch.float32).numpy(), float(inp["routed_scaling_factor"]))
+    ids = want["ids"]
+    got_ids = ops_mod.route(inp["routing_logits"].to(torch.float32).contiguous(),
+                            inp["routing_bias"].to(torch.float32).contiguous(), float(inp["routed_scaling_factor"]),
+                            int(inp["local_expert_offset"]))["topk_ids"].cpu().numpy()
+    assert np.array_equal(got_ids, ids)
+    off = int(inp["local_expert_offset"])
+    toks = sorted(set(_sample_tokens(ids, off, seed=T)) | _fragment_boundary_tokens(ids, off))
+    _check_against_models(f"builder T={T}[{len(toks)} tokens]", out, inp_cpu, token_subset=toks)
+    local = ((ids >= off) & (ids < off + 32)).any(1)
+    outf = out.float()
+    assert torch.count_nonzero(outf[torch.from_numpy(~local).to(cuda)]).item() == 0
+    assert torch.count_nonzero(outf[torch.from_numpy(local).to(cuda)].abs().sum(1) == 0).item() == 0
+    assert bool(torch.isfinite(outf).all())
+    out2 = layer.run_custom(ops_mod, **inp)
+    assert torch.equal(out.view(torch.int16), out2.view(torch.int16))
+
+
 def test_reference_builder_fixture_T8(cuda):
     """Against the real reference.run output for the reference builder at
     T=8, seed 8 (inputs drawn on the CPU generator, as recorded)."""
@@ -306,11 +420,12 @@ def test_forward_fewer_local_experts(ops, cuda):
     _check_against_models("E_local=8", out, _cpu(inp))
 
 
-@pytest.mark.parametrize("T", [128, 640])
+@pytest.mark.parametrize("T", [17, 64, 128, 640])
 def test_forward_every_token_on_the_same_experts(ops, cuda, T):
     """Every token picks experts 0..7: eight local experts hold T routes each
-    (the decode path's largest route count per expert at T=128, and
-    several full route tiles per expert on the prefill path at T=640)."""
+    (T=17 and 64: several passes of the decode kernels' one-fragment loop;
+    T=128: the decode path's largest route count per expert, two-fragment
+    passes; T=640: several full route tiles per expert on the prefill path)."""
     from conftest import pkg
 
     layer = pkg("moe_layer")
