@@ -50,6 +50,11 @@ SIGNATURES = {
         [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_float, _c_int, _c_int, _c_int, _c_vp, _c_size,
          _c_vp, _c_vp, ctypes.POINTER(_c_vp), _c_int],
     ),
+    "moe_noalloc_scratch_bytes": (_c_size, []),
+    "moe_forward_noalloc": (
+        _c_int,
+        [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_float, _c_int, _c_int, _c_int, _c_vp, _c_vp],
+    ),
     "moe_route": (_c_int, [_c_vp, _c_vp, _c_float, _c_int, _c_int, _c_int, _c_vp, _c_size, _c_vp]),
     "moe_packed_router_bytes": (_c_size, []),
     "moe_pack_router": (_c_int, [_c_vp, _c_vp, _c_vp]),

@@ -6,6 +6,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -94,6 +95,33 @@ int route_and_dispatch(const float* logits, const float* bias, float rsf, int of
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]), st),
                      "dispatch kernels launch"));
+  return MOE_OK;
+}
+
+// Workspace of moe_forward_noalloc: device memory of the library itself, one
+// copy per GPU, held until the process ends.  In host code `scratch` names a
+// host-side stand-in for the symbol, never the device memory: its device
+// address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) uint8_t scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_of[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device, with that device current).
+int scratch_address(void** ptr) {
+  int dev = 0;
+  MOE_TRY(hip_status(hipGetDevice(&dev), "hipGetDevice"));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MOE_ERR_INVALID_ARG, "device %d beyond the %d supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_of[dev]) {
+    void* p = nullptr;
+    MOE_TRY(hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    if (!p) return fail(MOE_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch_of[dev] = p;
+  }
+  *ptr = g_scratch_of[dev];
   return MOE_OK;
 }
 
@@ -255,6 +283,29 @@ int moe_forward(const void* hidden, const float* hidden_scale, const void* w13_p
                 size_t workspace_bytes, void* out_bf16, void* stream) {
   return forward_impl(hidden, hidden_scale, w13_packed, w13_scale, w2_packed, w2_scale, logits, bias,
                       routed_scaling_factor, local_expert_offset, T, e_local, workspace, workspace_bytes, out_bf16,
+                      stream, nullptr, 0);
+}
+
+size_t moe_noalloc_scratch_bytes(void) { return MOE_NOALLOC_SCRATCH_BYTES; }
+
+int moe_forward_noalloc(const void* hidden, const float* hidden_scale, const void* w13_packed, const float* w13_scale,
+                        const void* w2_packed, const float* w2_scale, const float* logits, const float* bias,
+                        float routed_scaling_factor, int local_expert_offset, int T, int e_local, void* out_bf16,
+                        void* stream) {
+  // Sizes first: nothing touches the GPU for a call that cannot fit.
+  if (T < 0 || T > MOE_MAX_T) return fail(MOE_ERR_INVALID_ARG, "T must be in [0, %d], got %d", MOE_MAX_T, T);
+  MOE_TRY(check_e_local(e_local));
+  const size_t need = layout(T, e_local, nullptr);
+  if (need > MOE_NOALLOC_SCRATCH_BYTES)
+    return fail(MOE_ERR_WORKSPACE,
+                "moe_forward_noalloc: T=%d with e_local=%d needs %zu bytes of scratch, more than its fixed %zu "
+                "(use moe_forward with a caller workspace)",
+                T, e_local, need, (size_t)MOE_NOALLOC_SCRATCH_BYTES);
+  if (T == 0) return MOE_OK;
+  void* ws = nullptr;
+  MOE_TRY(scratch_address(&ws));
+  return forward_impl(hidden, hidden_scale, w13_packed, w13_scale, w2_packed, w2_scale, logits, bias,
+                      routed_scaling_factor, local_expert_offset, T, e_local, ws, MOE_NOALLOC_SCRATCH_BYTES, out_bf16,
                       stream, nullptr, 0);
 }
 

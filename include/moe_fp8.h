@@ -107,6 +107,27 @@ int moe_forward(const void* hidden, const float* hidden_scale, const void* w13_p
                 size_t workspace_bytes, void* out_bf16, void* stream);
 
 /*
+ * moe_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The workspace is the library's own device array of
+ * MOE_NOALLOC_SCRATCH_BYTES (moe_noalloc_scratch_bytes()), one per GPU,
+ * held until the process ends; the call allocates and frees nothing.
+ * (T, e_local) whose moe_workspace_bytes() exceeds it are rejected with
+ * MOE_ERR_WORKSPACE before any GPU work: T <= 128 always fits.  Every call
+ * on one GPU uses that GPU's one array, so calls that overlap on a GPU (on
+ * different streams, or from different threads) race and must be
+ * serialised by the caller.  Nothing in the array needs clearing between
+ * calls: every buffer is fully written before it is read.
+ */
+#define MOE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+size_t moe_noalloc_scratch_bytes(void);
+int moe_forward_noalloc(const void* hidden, const float* hidden_scale, const void* w13_packed,
+                        const float* w13_scale, const void* w2_packed, const float* w2_scale, const float* logits,
+                        const float* bias, float routed_scaling_factor, int local_expert_offset, int T,
+                        int e_local, void* out_bf16, void* stream);
+
+/*
  * moe_forward that also records events[0..5] (hipEvent_t handles created by
  * the caller) on `stream` before the route, dispatch, GEMM1, GEMM2 and
  * combine launches and after the last one, so each kernel can be timed on

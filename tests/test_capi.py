@@ -136,3 +136,16 @@ def test_host_generator_threads_agree(ops):
     a = ops.host_normal_e4m3(3_000_001, 11, 3, threads=1)
     b = ops.host_normal_e4m3(3_000_001, 11, 3, threads=7)
     assert np.array_equal(a, b)
+
+
+def test_noalloc_validation_before_any_gpu_work(lib, capi):
+    """moe_forward_noalloc rejects sizes beyond its fixed scratch (and bad
+    sizes) from the host, before touching the GPU; T == 0 is a no-op."""
+    assert lib.moe_noalloc_scratch_bytes() == 32 << 20
+    assert lib.moe_workspace_bytes(128, 32) <= lib.moe_noalloc_scratch_bytes()
+    null = ctypes.c_void_p(0)
+    rc = lib.moe_forward_noalloc(*([null] * 8), 1.0, 0, 8192, 32, null, null)
+    assert rc == capi.MOE_ERR_WORKSPACE and b"scratch" in lib.moe_last_error()
+    assert lib.moe_forward_noalloc(*([null] * 8), 1.0, 0, -1, 32, null, null) == capi.MOE_ERR_INVALID_ARG
+    assert lib.moe_forward_noalloc(*([null] * 8), 1.0, 0, 16, 0, null, null) == capi.MOE_ERR_INVALID_ARG
+    assert lib.moe_forward_noalloc(*([null] * 8), 1.0, 0, 0, 32, null, null) == capi.MOE_OK
