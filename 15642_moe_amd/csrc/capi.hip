@@ -254,7 +254,8 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
                        "stage1_decode_kernel launch"));
     MOE_TRY(mark(3));
     MOE_TRY(hip_status(moe::launch_stage2_decode(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts,
-                                                 offsets, route_weight, Y, e_local, T, st),
+                                                 offsets, route_weight, route_token, Y,
+                                                 static_cast<uint16_t*>(out_bf16), e_local, T, st),
                        "stage2_decode_kernel launch"));
   } else {
     MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, local_expert_offset, counts, offsets,
@@ -267,7 +268,8 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
                        "stage1_kernel launch"));
     MOE_TRY(mark(3));
     MOE_TRY(hip_status(moe::launch_stage2(Cq, Cs, static_cast<const uint8_t*>(w2_packed), w2_scale, counts, offsets,
-                                          route_weight, Y, T, e_local, R, queue + moe::QUEUE_COUNTERS / 2, st),
+                                          route_weight, route_token, Y, static_cast<uint16_t*>(out_bf16), T, e_local,
+                                          R, queue + moe::QUEUE_COUNTERS / 2, st),
                        "stage2_kernel launch"));
   }
   MOE_TRY(mark(4));

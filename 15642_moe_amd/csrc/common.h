@@ -60,6 +60,15 @@ __device__ __forceinline__ v4f mfma_16x16x128_fp8(const v8i& a, const v8i& b, co
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// D = A(32x64 fp8) * B(64x32 fp8) + C, fp32: v_mfma_f32_32x32x64_f8f6f4 (no
+// block scale).  Lane l holds row (A) / column (B) l % 32, K bytes
+// [32*(l/32), 32*(l/32)+32) as 8 dwords; D register r of lane l is row
+// 8*(r/4) + 4*(l/32) + r%4, column l % 32.
+typedef float v16f __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ v16f mfma_32x32x64_fp8(const v8i& a, const v8i& b, const v16f& c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
 // OCP E4M3FN encode, round-to-nearest-even.  |x| > 464 and NaN give 0x7F
 // (NaN) unless `sat`, in which case finite overflow saturates to 448.
 // Written from the OCP 8-bit floating point specification (v1.0).
@@ -84,11 +93,25 @@ __host__ __device__ __forceinline__ uint16_t bf16_rne(float x) {
   return (uint16_t)((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
 }
 
+// The output of a token with a single local route: bf16 RNE of (0 + y), the
+// combine's sum over one route (0 + -0 is +0), four columns at once.
+__device__ __forceinline__ void store_out_bf16x4(uint16_t* dst, float4 v) {
+  uint2 o;
+  o.x = (uint32_t)bf16_rne(v.x + 0.0f) | ((uint32_t)bf16_rne(v.y + 0.0f) << 16);
+  o.y = (uint32_t)bf16_rne(v.z + 0.0f) | ((uint32_t)bf16_rne(v.w + 0.0f) << 16);
+  *reinterpret_cast<uint2*>(dst) = o;
+}
+
 // Two floats -> two e4m3 bytes (low half of the result), hardware
 // v_cvt_pk_fp8_f32: RNE, non-saturating; callers clamp to +-448 first.
 __device__ __forceinline__ uint32_t cvt2_e4m3(float a, float b) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
 }
+
+// Flag in route_token: the route is its token's only local route (the GEMM2
+// kernels then write the token's output row, and the combine skips it).
+constexpr int SINGLE_ROUTE_BIT = (int)0x80000000u;
+constexpr int ROUTE_TOKEN_MASK = 0x7FFFFFFF;
 
 // Bit le is set when the token (its 8 picks in ids) picked global expert
 // le + offset; 1 <= e_local <= 32.

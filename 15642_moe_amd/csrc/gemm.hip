@@ -13,7 +13,8 @@
 // quant_kernel : per-(route, 128-I-block) dynamic FP8 requant
 //     C = e4m3(c / max(amax/448, 1e-8)) (moe.cu:516-541).
 // stage2_decode_kernel : O = C x W2_e^T with C_scale x W2 block scales
-//     (moe.cu:547-686, moe_ref.py:75-79,131), Y = O * weight.
+//     (moe.cu:547-686, moe_ref.py:75-79,131), y = O * weight, to Y or, for
+//     a token with a single local route, to its bf16 output row.
 #include "common.h"
 #include "gemm_util.h"
 #include "launch.h"
@@ -137,7 +138,7 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         int kpos = 0;
 #pragma unroll
         for (int k = 0; k < TOP_K; ++k) kpos = (ids[k] == e + offset) ? k : kpos;
-        route_token[r] = t;
+        route_token[r] = t | (__popc(mask[c]) == 1 ? SINGLE_ROUTE_BIT : 0);
         route_weight[r] = topk_w[(size_t)t * TOP_K + kpos];
         token_route[(size_t)t * TOP_K + __popc(mask[c] & ((1u << e) - 1u))] = r;
       }
@@ -270,7 +271,8 @@ __global__ void __launch_bounds__(64)
 stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
                      const float* __restrict__ w2s, const int32_t* __restrict__ counts,
                      const int32_t* __restrict__ offsets, const float* __restrict__ route_weight,
-                     float* __restrict__ Y, int e_local) {
+                     const int32_t* __restrict__ route_token, float* __restrict__ Y, uint16_t* __restrict__ out,
+                     int e_local) {
   constexpr int BM = 16, NSLICE = H / 64;
   static_assert(IB % NR == 0, "ring depth must divide the K-block count");
   const int lane = threadIdx.x;
@@ -352,11 +354,20 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
       if (col < rows[f]) {
         const int r = off + m0 + f * BM + col;
         const float rw = route_weight[r];
-        float* yrow = Y + (size_t)r * H + hb * BLK + 16 * t0 + 4 * (lane >> 4);
+        // a route whose token has no other local route writes its bf16
+        // output row itself (the combine skips such tokens)
+        const int rt = route_token[r];
+        const bool single = rt < 0;  // SINGLE_ROUTE_BIT
+        const int tok = rt & ROUTE_TOKEN_MASK;
+        const size_t c0 = (size_t)hb * BLK + 16 * t0 + 4 * (lane >> 4);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const v4f y = acc[f][i] * rw;
-          *reinterpret_cast<float4*>(yrow + 16 * i) = make_float4(y[0], y[1], y[2], y[3]);
+          const float4 v = make_float4(y[0], y[1], y[2], y[3]);
+          if (single)
+            store_out_bf16x4(out + (size_t)tok * H + c0 + 16 * i, v);
+          else
+            *reinterpret_cast<float4*>(Y + (size_t)r * H + c0 + 16 * i) = v;
         }
       }
     }
@@ -416,15 +427,16 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
 }
 
 hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
-                                const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
-                                int e_local, int T, hipStream_t stream) {
+                                const int32_t* counts, const int32_t* offsets, const float* route_weight,
+                                const int32_t* route_token, float* Y, uint16_t* out, int e_local, int T,
+                                hipStream_t stream) {
   const int grid = e_local * (H / 64);
   if (T > 64)  // as stage 1: two fragments per weight pass
-    stage2_decode_kernel<4, 2><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
-                                                        e_local);
+    stage2_decode_kernel<4, 2><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight,
+                                                        route_token, Y, out, e_local);
   else
-    stage2_decode_kernel<4, 1><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, Y,
-                                                        e_local);
+    stage2_decode_kernel<4, 1><<<grid, 64, 0, stream>>>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight,
+                                                        route_token, Y, out, e_local);
   return hipGetLastError();
 }
 

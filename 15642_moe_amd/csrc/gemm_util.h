@@ -62,6 +62,22 @@ __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const 
   mt = local - blk * nt;
 }
 
+// Routes of route tile mt of expert e: [m0, m0 + rows).  The expert's
+// 32-route pairs of MFMA fragments, ceil(count / 32), are dealt evenly over
+// its s_tp[e+1] - s_tp[e] tiles (each gets floor or ceil of the share, at
+// most BM / 32 since the tile count is ceil(count / BM) and BM is a multiple
+// of 32), so all tiles of an expert do the same work and the tiles that
+// stream one weight block stay in step, instead of a short last tile running
+// ahead.  Pairs, because the K loop's route-tile counts are instantiated in
+// pairs: an odd count would compute a padding fragment.
+__device__ __forceinline__ void tile_routes(int e, int mt, const int* s_tp, const int* s_cnt, int& m0, int& rows) {
+  const int nt = s_tp[e + 1] - s_tp[e];
+  const int cnt = s_cnt[e];
+  const int q = (cnt + 31) >> 5;
+  m0 = 32 * ((mt * q) / nt);
+  rows = min(cnt, 32 * (((mt + 1) * q) / nt)) - m0;
+}
+
 // ---------------------------------------------------------------------------
 // Host side.
 // ---------------------------------------------------------------------------

@@ -14,6 +14,8 @@ int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream);
+// Output rows of tokens with zero or several local routes (the GEMM2 kernels
+// write the rows of tokens with exactly one).
 hipError_t launch_combine(const float* Y, const int32_t* token_route, int T, uint16_t* out,
                           hipStream_t stream);
 
@@ -31,7 +33,8 @@ hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const
                          int max_routes, int32_t* queue, hipStream_t stream);
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
-                         float* Y, int T, int e_local, int max_routes, int32_t* queue, hipStream_t stream);
+                         const int32_t* route_token, float* Y, uint16_t* out, int T, int e_local, int max_routes,
+                         int32_t* queue, hipStream_t stream);
 
 // Decode path (T <= DECODE_MAX_T): GEMM1 + SwiGLU with the local dispatch
 // fused in (fp32 output Cf), the FP8 requant, then GEMM2 over 64-row items.
@@ -41,8 +44,9 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
                                 float* route_weight, int32_t* token_route, float* Cf, uint8_t* Cq, float* Cs,
                                 hipStream_t stream);
 hipError_t launch_stage2_decode(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
-                                const int32_t* counts, const int32_t* offsets, const float* route_weight, float* Y,
-                                int e_local, int T, hipStream_t stream);
+                                const int32_t* counts, const int32_t* offsets, const float* route_weight,
+                                const int32_t* route_token, float* Y, uint16_t* out, int e_local, int T,
+                                hipStream_t stream);
 
 // Producer of the forward's inputs (router logits + FP8 activations) from
 // bf16 hidden states; `partial` holds router_partial_bytes(T) (unused when 0).

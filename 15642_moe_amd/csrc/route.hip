@@ -3,9 +3,10 @@
 // route_kernel     : no-aux-loss DeepSeek routing, one wave64 per token
 //                    (semantics of reference/moe_ref.py:81-107; the reference
 //                    kernel is route_dispatch_kernel, kernels/moe.cu:213-329).
-// dispatch_count_kernel, dispatch_place_kernel : deterministic token-ordered
-//                    compaction of the local (token, expert) pairs into
-//                    per-expert route lists, one workgroup per 256-token chunk.
+// dispatch_count_kernel + dispatch_place_kernel :
+//                    deterministic token-ordered compaction of the local
+//                    (token, expert) pairs into per-expert route lists, one
+//                    wave per 64-token chunk.
 // combine_kernel   : per-token sum of the weighted per-route expert outputs in
 //                    ascending expert order, then bf16 RNE (the reference does
 //                    fp32 atomics + bf16_convert_kernel, kernels/moe.cu:682,688-695;
@@ -32,6 +33,33 @@ __device__ __forceinline__ uint32_t order_key(float v) {
 
 __device__ __forceinline__ int popc(uint64_t m) { return __popcll(m); }
 
+// Cross-lane moves by DPP (no LDS round trip): quad_perm [1,0,3,2] and
+// [2,3,0,1] pair lanes l ^ 1 and l ^ 2, row_half_mirror l ^ 7 within 8
+// lanes, row_mirror l ^ 15 within a 16-lane row; row_bcast:15 / :31 copy
+// the last lane of the row below into rows 1, 3 / 2, 3 (lanes outside the
+// row mask keep their own value).
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
+constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(x)));
+}
+
+// Maximum over the wave's 64 lanes (wave-uniform result).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, dpp_u32<DPP_XOR1>(x));
+  x = max(x, dpp_u32<DPP_XOR2>(x));
+  x = max(x, dpp_u32<DPP_HALF_MIRROR>(x));
+  x = max(x, dpp_u32<DPP_MIRROR>(x));            // every lane of a row: the row's max
+  x = max(x, dpp_u32<DPP_BCAST15, 0xA>(x));      // rows 1, 3: max of rows 0-1, 2-3
+  x = max(x, dpp_u32<DPP_BCAST31, 0xC>(x));      // row 3: max of rows 0-3
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 __global__ void __launch_bounds__(256)
 route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, float rsf, int T,
              int32_t* __restrict__ topk_ids, float* __restrict__ topk_w) {
@@ -56,13 +84,16 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
     if (v[j] > m1) { m2 = m1; m1 = v[j]; }
     else if (v[j] > m2) { m2 = v[j]; }
   }
-#pragma unroll
-  for (int off = 1; off < 8; off <<= 1) {
-    const float o1 = __shfl_xor(m1, off), o2 = __shfl_xor(m2, off);
+  // merge with the lanes l ^ 1, l ^ 2, then l ^ 7: all 8 lanes of the group
+  // end with its two largest scores
+  auto merge = [&](float o1, float o2) {
     const float n2 = fmaxf(fminf(m1, o1), fmaxf(m2, o2));
     m1 = fmaxf(m1, o1);
     m2 = n2;
-  }
+  };
+  merge(dpp_f32<DPP_XOR1>(m1), dpp_f32<DPP_XOR1>(m2));
+  merge(dpp_f32<DPP_XOR2>(m1), dpp_f32<DPP_XOR2>(m2));
+  merge(dpp_f32<DPP_HALF_MIRROR>(m1), dpp_f32<DPP_HALF_MIRROR>(m2));
   const float gscore = m1 + m2;
 
   // Top-4 groups: rank by (score desc, group index asc).
@@ -70,40 +101,33 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   int rank = 0;
 #pragma unroll
   for (int g = 0; g < N_GROUP; ++g) {
-    const float gs = __shfl(gscore, g * 8);
+    const float gs = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), g * 8));
     rank += (gs > gscore || (gs == gscore && g < my_g)) ? 1 : 0;
   }
   const bool group_sel = rank < TOPK_GROUP;
 
-  // Top-8 experts of the kept groups by (value desc, index asc): the 8th
-  // largest key is found bit by bit from wave-wide ballot counts, then ties
-  // at that key are filled in ascending expert order.
+  // Top-8 experts of the kept groups by (value desc, index asc): eight
+  // rounds of a wave-wide max of the lanes' best remaining key; ties at the
+  // maximum go to the lowest lane (lowest experts), and within that lane to
+  // its lowest expert.  The picked key is cleared for the next round.
   uint32_t key[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) key[j] = group_sel ? order_key(v[j]) : 0u;
-  uint32_t thr = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int cnt = 0;
+  bool sel[4] = {false, false, false, false};
+#pragma unroll 1
+  for (int k = 0; k < TOP_K; ++k) {
+    const uint32_t lk = max(max(key[0], key[1]), max(key[2], key[3]));
+    const uint32_t M = wave_max_u32(lk);
+    const uint64_t bal = __ballot(lk == M);
+    const int win = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(bal));
+    if (lane == win) {
+      const int j = key[0] == M ? 0 : key[1] == M ? 1 : key[2] == M ? 2 : 3;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cnt += popc(__ballot(key[j] >= cand));
-    if (cnt >= TOP_K) thr = cand;
+      for (int jj = 0; jj < 4; ++jj)
+        if (jj == j) { sel[jj] = true; key[jj] = 0u; }
+    }
   }
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int n_gt = 0, eq_seen = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    n_gt += popc(__ballot(key[j] > thr));
-    eq_seen += popc(__ballot(key[j] == thr) & below);
-  }
-  const int need = TOP_K - n_gt;
-  bool sel[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool eq = key[j] == thr;
-    sel[j] = key[j] > thr || (eq && eq_seen < need);
-    eq_seen += eq ? 1 : 0;
-  }
   // Position in ascending expert order = selected experts below this one.
   int pos = 0;
 #pragma unroll
@@ -128,215 +152,152 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   }
 }
 
-// Local dispatch in two passes over chunks of 256 tokens (one workgroup
-// each): dispatch_count_kernel writes every chunk's per-expert pick counts,
-// dispatch_place_kernel sums the counts of the chunks before its own (its
-// per-expert base) and ranks its tokens per expert with wave ballots, so
-// slots follow token order (a stable counting sort) and the dispatch is
-// deterministic.  Route r of expert e lives at offsets[e] + slot.
-constexpr int DISPATCH_CHUNK = 256;
-constexpr int DISPATCH_WAVES = DISPATCH_CHUNK / 64;
+// Local dispatch: a stable counting sort of the local (token, expert) picks
+// into per-expert route lists, so route r = offsets[e] + slot with slots in
+// token order (deterministic; the reference appends in atomic order,
+// kernels/moe.cu:313-321).  Tokens come in chunks of 64, one wave each: a
+// chunk's per-expert counts are wave ballots, and a chunk's first slot per
+// expert is the expert's offset plus the counts of the chunks before it:
+// dispatch_count_kernel writes every chunk's counts and dispatch_place_kernel
+// sums those of the chunks before its own.  One wave per workgroup spreads
+// the chunks (and their scattered stores) over the CUs; a single workgroup
+// holding every chunk of T = 1024 took 16 us, all its stores on one CU.
+constexpr int DISPATCH_CHUNK = 64;
 
-// Picks of this thread's token (0 past T) as a local-expert bit mask.
-__device__ __forceinline__ uint32_t chunk_token_mask(const int32_t* __restrict__ topk_ids, int T, int offset,
-                                                     int e_local) {
-  const int t = blockIdx.x * DISPATCH_CHUNK + threadIdx.x;
-  return t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
+// Expert e's pick count among the wave's tokens (bit e of m), in lane e.
+__device__ __forceinline__ int wave_expert_counts(uint32_t m, int e_local, int lane) {
+  int mine = 0;
+  for (int e = 0; e < e_local; ++e) {
+    const int c = __popcll(__ballot((m >> e) & 1u));
+    mine = lane == e ? c : mine;
+  }
+  return mine;
 }
 
-// Writes token t's local routes (its bit mask m over local experts): route
-// r = s_base[e] + wave_off[e] + (lanes below this one in the wave that also
-// picked e), so slots follow token order within each expert; token_route
-// lists the routes in ascending expert order, -1 after the last.
-__device__ __forceinline__ void place_token(uint32_t m, const int* ids, const float* ws, int t, bool valid, int offset,
-                                            int e_local, const int* s_base, const int* wave_off, int lane,
-                                            int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                                            int32_t* __restrict__ token_route) {
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int j = 0;
+// The wave's ballots per expert, into s_bal[0 .. e_local).
+__device__ __forceinline__ void wave_expert_ballots(uint32_t m, int e_local, int lane, uint64_t* s_bal) {
   for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
+    const uint64_t b = __ballot((m >> e) & 1u);
+    if (lane == 0) s_bal[e] = b;
+  }
+}
+
+// Writes the routes of the wave's 64 tokens (this lane: token t, local-pick
+// mask m): token_route rows start as -1; then for every expert e that a
+// token of the wave picked, the lanes that picked it take slots base[e] +
+// (lanes below with the same pick), so consecutive lanes write consecutive
+// routes (one contiguous run per expert and store) in token order.  The
+// token's routes land in token_route in ascending expert order, and
+// route_token carries SINGLE_ROUTE_BIT for a token's only local route.
+__device__ __forceinline__ void place_wave(const int* ids, const float* ws, uint32_t m, int t, bool valid, int offset,
+                                           int e_local, const int* base, const uint64_t* bal, int lane,
+                                           int32_t* __restrict__ route_token, float* __restrict__ route_weight,
+                                           int32_t* __restrict__ token_route) {
+  if (valid) {
+    int4* row = reinterpret_cast<int4*>(token_route + (size_t)t * TOP_K);
+    row[0] = make_int4(-1, -1, -1, -1);
+    row[1] = make_int4(-1, -1, -1, -1);
+  }
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int tag = t | (__popc(m) == 1 ? SINGLE_ROUTE_BIT : 0);
+  for (int e = 0; e < e_local; ++e) {
+    const uint64_t b = bal[e];
+    if (b == 0) continue;  // wave-uniform
     if ((m >> e) & 1u) {
-      const int r = s_base[e] + wave_off[e] + __popcll(bal & lt_mask);
+      const int r = base[e] + __popcll(b & lt_mask);
       float wsel = 0.0f;
 #pragma unroll
-      for (int k = 0; k < TOP_K; ++k)
-        if (ids[k] - offset == e) wsel = ws[k];
-      route_token[r] = t;
+      for (int k = 0; k < TOP_K; ++k) wsel = (ids[k] == e + offset) ? ws[k] : wsel;
+      route_token[r] = tag;
       route_weight[r] = wsel;
-      token_route[(size_t)t * TOP_K + j] = r;
-      ++j;
+      token_route[(size_t)t * TOP_K + __popc(m & ((1u << e) - 1u))] = r;
     }
   }
-  if (valid)
-    for (; j < TOP_K; ++j) token_route[(size_t)t * TOP_K + j] = -1;
 }
 
-__global__ void __launch_bounds__(DISPATCH_CHUNK)
+// This lane's token (t < T) picks and weights.
+__device__ __forceinline__ uint32_t load_picks(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w,
+                                               int t, bool valid, int offset, int e_local, int* ids, float* ws) {
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k) {
+    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
+    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
+  }
+  return valid ? local_mask(ids, offset, e_local) : 0u;
+}
+
+// Lanes 0..31 of one wave: expert e = lane's total `tot` -> exclusive scan
+// over experts (offsets), published by `publish`; returns offsets[e].
+__device__ __forceinline__ int expert_offsets(int tot, int lane, int e_local, bool publish, int32_t* __restrict__ counts,
+                                              int32_t* __restrict__ offsets) {
+  const bool live = lane < e_local;
+  tot = live ? tot : 0;
+  int inc = tot;
+#pragma unroll
+  for (int d = 1; d < MAX_E_LOCAL; d <<= 1) {
+    const int o = __shfl_up(inc, d, MAX_E_LOCAL);
+    if ((lane & (MAX_E_LOCAL - 1)) >= d) inc += o;
+  }
+  const int excl = inc - tot;
+  if (publish && live) {
+    counts[lane] = tot;
+    offsets[lane] = excl;
+    if (lane == e_local - 1) offsets[e_local] = inc;
+  }
+  return excl;
+}
+
+// Pass 1: chunk c's per-expert counts into chunk_counts[c][32].
+__global__ void __launch_bounds__(64)
 dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T, int e_local, int offset,
                       int32_t* __restrict__ chunk_counts, int32_t* __restrict__ queue) {
-  __shared__ int s_wtot[DISPATCH_WAVES][MAX_E_LOCAL];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // The GEMM launches that follow take work from these counters.
-  if (blockIdx.x == 0 && tid < QUEUE_COUNTERS) queue[tid] = 0;
-  const uint32_t m = chunk_token_mask(topk_ids, T, offset, e_local);
-  for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
-    if (lane == 0) s_wtot[wave][e] = __popcll(bal);
-  }
-  __syncthreads();
-  if (tid < e_local) {
-    int c = 0;
-#pragma unroll
-    for (int w = 0; w < DISPATCH_WAVES; ++w) c += s_wtot[w][tid];
-    chunk_counts[(size_t)blockIdx.x * MAX_E_LOCAL + tid] = c;
-  }
+  const int lane = threadIdx.x;
+  if (blockIdx.x == 0 && lane < QUEUE_COUNTERS) queue[lane] = 0;  // work queues of the GEMMs that follow
+  const int t = blockIdx.x * DISPATCH_CHUNK + lane;
+  const uint32_t m = t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
+  const int c = wave_expert_counts(m, e_local, lane);
+  if (lane < MAX_E_LOCAL) chunk_counts[(size_t)blockIdx.x * MAX_E_LOCAL + lane] = lane < e_local ? c : 0;
 }
 
-__global__ void __launch_bounds__(DISPATCH_CHUNK)
-dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T,
-                      int e_local, int offset, const int32_t* __restrict__ chunk_counts,
-                      int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                      int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                      int32_t* __restrict__ token_route) {
-  constexpr int NWAVE = DISPATCH_WAVES;
-  constexpr int CSTEP = DISPATCH_CHUNK / MAX_E_LOCAL;
-  __shared__ int s_part[2][DISPATCH_CHUNK];
+// Pass 2: chunk c's first slot per expert = offsets[e] + counts of chunks
+// before c (lane e sums the even chunks, lane 32 + e the odd ones), then its
+// tokens' routes.
+__global__ void __launch_bounds__(64)
+dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
+                      int offset, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+                      int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
+                      float* __restrict__ route_weight, int32_t* __restrict__ token_route) {
   __shared__ int s_base[MAX_E_LOCAL];
-  __shared__ int s_wtot[NWAVE][MAX_E_LOCAL], s_woff[NWAVE][MAX_E_LOCAL];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c0 = blockIdx.x * DISPATCH_CHUNK;
-  const int nchunks = gridDim.x;
-
-  // The token's picks and the chunk counts are loaded up front, so the two
-  // load latencies overlap; nothing below waits on memory again.
-  const int t = c0 + tid;
+  __shared__ uint64_t s_bal[MAX_E_LOCAL];
+  const int lane = threadIdx.x, c = blockIdx.x, nchunks = gridDim.x;
+  const int t = c * DISPATCH_CHUNK + lane;
   const bool valid = t < T;
   int ids[TOP_K];
   float ws[TOP_K];
-#pragma unroll
-  for (int k = 0; k < TOP_K; ++k) {
-    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
-    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
+  const uint32_t m = load_picks(topk_ids, topk_w, t, valid, offset, e_local, ids, ws);
+  const int e = lane & (MAX_E_LOCAL - 1);
+  int pre = 0, tot = 0;
+#pragma unroll 8
+  for (int cc = lane >> 5; cc < nchunks; cc += 2) {
+    const int v = chunk_counts[(size_t)cc * MAX_E_LOCAL + e];
+    pre += cc < c ? v : 0;
+    tot += v;
   }
-  {  // picks of expert tid % 32 in chunks tid/32, tid/32 + 8, ..., before this chunk and in total
-    const int e = tid % MAX_E_LOCAL;
-    int pre = 0, tot = 0;
-#pragma unroll 4
-    for (int c = tid / MAX_E_LOCAL; c < nchunks; c += CSTEP) {
-      const int v = e < e_local ? chunk_counts[(size_t)c * MAX_E_LOCAL + e] : 0;
-      pre += c < (int)blockIdx.x ? v : 0;
-      tot += v;
-    }
-    s_part[0][tid] = pre;
-    s_part[1][tid] = tot;
-  }
-  const uint32_t m = valid ? local_mask(ids, offset, e_local) : 0u;
-  for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
-    if (lane == 0) s_wtot[wave][e] = __popcll(bal);
-  }
+  pre += __shfl_xor(pre, 32);
+  tot += __shfl_xor(tot, 32);
+  const int excl = expert_offsets(tot, lane, e_local, c == 0 && lane < MAX_E_LOCAL, counts, offsets);
+  if (lane < MAX_E_LOCAL) s_base[lane] = excl + pre;
+  wave_expert_ballots(m, e_local, lane, s_bal);
   __syncthreads();
-  if (tid < MAX_E_LOCAL) {
-    // Lane e of wave 0: expert e's picks before this chunk and in total, the
-    // exclusive scan of the totals over experts (offsets[e]) by shuffles,
-    // and the waves' offsets inside this chunk.
-    const bool live = tid < e_local;
-    int pre = 0, tot = 0;
-#pragma unroll
-    for (int j = 0; j < CSTEP; ++j) {
-      pre += s_part[0][j * MAX_E_LOCAL + tid];
-      tot += s_part[1][j * MAX_E_LOCAL + tid];
-    }
-    if (!live) pre = tot = 0;
-    int inc = tot;
-#pragma unroll
-    for (int d = 1; d < MAX_E_LOCAL; d <<= 1) {
-      const int o = __shfl_up(inc, d);
-      if (tid >= d) inc += o;
-    }
-    const int excl = inc - tot;
-    s_base[tid] = excl + pre;
-    if (blockIdx.x == 0 && live) {
-      counts[tid] = tot;
-      offsets[tid] = excl;
-      if (tid == e_local - 1) offsets[e_local] = inc;
-    }
-    int acc = 0;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) { s_woff[w][tid] = acc; acc += live ? s_wtot[w][tid] : 0; }
-  }
-  __syncthreads();
-  place_token(m, ids, ws, t, valid, offset, e_local, s_base, s_woff[wave], lane, route_token, route_weight,
-              token_route);
+  place_wave(ids, ws, m, t, valid, offset, e_local, s_base, s_bal, lane, route_token, route_weight, token_route);
 }
 
-// Up to DISPATCH_SMALL_T tokens (one chunk) the whole dispatch is one
-// workgroup of one thread per token (the same wave-ballot counting sort,
-// without the per-chunk counts and their launch); it also clears the GEMMs'
-// queue counters.  Measured on MI355X: T=160 11.3 us and T=256 12.1 us
-// against 15.3 / 16.1 us for the two launches; a 1024-thread version lost
-// at T=1024 (21 vs 16 us: one CU walking every expert for 16 waves).
-constexpr int DISPATCH_SMALL_T = DISPATCH_CHUNK;
-
-__global__ void __launch_bounds__(DISPATCH_SMALL_T)
-dispatch_small_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
-                      int offset, int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-                      int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                      int32_t* __restrict__ token_route, int32_t* __restrict__ queue) {
-  constexpr int NWAVE = DISPATCH_SMALL_T / 64;
-  __shared__ int s_woff[NWAVE][MAX_E_LOCAL];  // wave counts, then their exclusive offsets within the expert
-  __shared__ int s_base[MAX_E_LOCAL];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < QUEUE_COUNTERS) queue[tid] = 0;
-  const int t = tid;
-  const bool valid = t < T;
-  int ids[TOP_K];
-  float ws[TOP_K];
-#pragma unroll
-  for (int k = 0; k < TOP_K; ++k) {
-    ids[k] = valid ? topk_ids[(size_t)t * TOP_K + k] : -1;
-    ws[k] = valid ? topk_w[(size_t)t * TOP_K + k] : 0.0f;
-  }
-  const uint32_t m = valid ? local_mask(ids, offset, e_local) : 0u;
-  for (int e = 0; e < e_local; ++e) {
-    const uint64_t bal = __ballot((m >> e) & 1u);
-    if (lane == 0) s_woff[wave][e] = __popcll(bal);
-  }
-  __syncthreads();
-  if (tid < MAX_E_LOCAL) {
-    // Lane e of wave 0: expert e's waves in token order, then the exclusive
-    // scan of the totals over experts (offsets[e]) by shuffles.
-    const bool live = tid < e_local;
-    int tot = 0;
-#pragma unroll
-    for (int w = 0; w < NWAVE; ++w) {
-      const int c = live ? s_woff[w][tid] : 0;
-      s_woff[w][tid] = tot;
-      tot += c;
-    }
-    int inc = tot;
-#pragma unroll
-    for (int d = 1; d < MAX_E_LOCAL; d <<= 1) {
-      const int o = __shfl_up(inc, d);
-      if (tid >= d) inc += o;
-    }
-    const int excl = inc - tot;
-    s_base[tid] = excl;
-    if (live) {
-      counts[tid] = tot;
-      offsets[tid] = excl;
-      if (tid == e_local - 1) offsets[e_local] = inc;
-    }
-  }
-  __syncthreads();
-  place_token(m, ids, ws, t, valid, offset, e_local, s_base, s_woff[wave], lane, route_token, route_weight,
-              token_route);
-}
-
-// out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ).
-// Workgroup (t, part) covers 256 float4 columns of token t; the token's route
-// rows are loaded before any is used, so a launch costs one memory latency.
+// out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ),
+// zeros for a token without local routes.  Tokens with exactly one local
+// route are left alone: GEMM2 wrote their rows (bf16 of 0 + y, the same
+// bits).  Workgroup (t, part) covers 256 float4 columns of token t; the
+// token's route rows are loaded before any is used, so a launch costs one
+// memory latency.
 constexpr int COMBINE_PARTS = H / 4 / 256;  // 7
 
 __global__ void __launch_bounds__(256)
@@ -350,6 +311,7 @@ combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_ro
     r[k] = token_route[(size_t)t * TOP_K + k];
     n += r[k] >= 0 ? 1 : 0;  // valid routes come first
   }
+  if (n == 1) return;
   float4 y[TOP_K];
 #pragma unroll
   for (int k = 0; k < TOP_K; ++k)
@@ -376,18 +338,14 @@ int dispatch_chunks(int T) { return T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream) {
-  if (T <= DISPATCH_SMALL_T) {
-    dispatch_small_kernel<<<1, DISPATCH_SMALL_T, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, counts, offsets,
-                                                             route_token, route_weight, token_route, queue);
-    return hipGetLastError();
-  }
-  const int grid = dispatch_chunks(T);
+  const int nchunks = dispatch_chunks(T);
   int32_t* chunk_counts = queue + QUEUE_COUNTERS;
-  dispatch_count_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts, queue);
+  dispatch_count_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts, queue);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  dispatch_place_kernel<<<grid, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, chunk_counts,
-                                                             counts, offsets, route_token, route_weight, token_route);
+  dispatch_place_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, chunk_counts,
+                                                                counts, offsets, route_token, route_weight,
+                                                                token_route);
   return hipGetLastError();
 }
 

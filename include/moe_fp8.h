@@ -44,13 +44,14 @@ enum moe_ws_buffer {
   MOE_WS_TOPK_W,        /* f32   [T, 8]  routing weights (normalised * rsf)    */
   MOE_WS_COUNTS,        /* int32 [E]     routes per local expert               */
   MOE_WS_OFFSETS,       /* int32 [E+1]   first route of each local expert      */
-  MOE_WS_ROUTE_TOKEN,   /* int32 [R]     token of each route (token order)     */
+  MOE_WS_ROUTE_TOKEN,   /* int32 [R]     token of each route (token order);
+                           bit 31 set: the token's only local route            */
   MOE_WS_ROUTE_WEIGHT,  /* f32   [R]     routing weight of each route          */
   MOE_WS_TOKEN_ROUTE,   /* int32 [T, 8]  routes of each token, ascending, -1   */
   MOE_WS_CQ,            /* e4m3  [R, I]  SwiGLU output, block-quantised        */
   MOE_WS_CS,            /* f32   [R, 16] its per-128-block scales              */
   MOE_WS_Y,             /* f32   [R, H]  weighted expert outputs per route     */
-  MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/256)]  work-queue counters of the
+  MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/64)]  work-queue counters of the
                            prefill GEMMs (zeroed by the dispatch of every
                            forward), then the dispatch's per-chunk counts      */
   MOE_WS_NBUF

@@ -90,10 +90,16 @@ def route_bruteforce(logits: np.ndarray, bias: np.ndarray) -> np.ndarray:
     return np.asarray(out, dtype=np.int32)
 
 
+# route_token entries of routes whose token has no other local route carry
+# this bit (the GEMM2 kernels write those tokens' output rows themselves).
+SINGLE_ROUTE_FLAG = np.int32(-(2 ** 31))
+
+
 def local_dispatch(ids: np.ndarray, weights: np.ndarray, local_offset: int, e_local: int) -> dict:
     """Token-ordered per-expert route lists (the dispatch the GPU builds):
     route r of local expert e sits at offsets[e] + (rank of its token among
-    the expert's tokens)."""
+    the expert's tokens); route_token[r] is the token, with bit 31
+    (SINGLE_ROUTE_FLAG) set when that token has exactly one local route."""
     T = ids.shape[0]
     le = ids - int(local_offset)
     local = (le >= 0) & (le < e_local)
@@ -104,6 +110,7 @@ def local_dispatch(ids: np.ndarray, weights: np.ndarray, local_offset: int, e_lo
     route_weight = np.zeros(R, np.float32)
     token_route = np.full((T, TOP_K), -1, np.int32)
     fill = offsets[:-1].copy()
+    n_local = local.sum(axis=1)
     for t in range(T):
         j = 0
         for k in range(TOP_K):  # ids ascending -> local experts ascending
@@ -111,7 +118,8 @@ def local_dispatch(ids: np.ndarray, weights: np.ndarray, local_offset: int, e_lo
                 e = le[t, k]
                 r = fill[e]
                 fill[e] += 1
-                route_token[r] = t
+                # bit 31 flags the route of a token with a single local route
+                route_token[r] = t | (SINGLE_ROUTE_FLAG if n_local[t] == 1 else 0)
                 route_weight[r] = weights[t, k]
                 token_route[t, j] = r
                 j += 1

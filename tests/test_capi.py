@@ -48,7 +48,7 @@ def test_workspace_layout(lib, capi, T, E):
     off = capi.workspace_offsets(T, E)
     R = T * min(8, E)
     sizes = [T * 32, T * 32, E * 4, (E + 1) * 4, R * 4, R * 4, T * 32, R * 2048, R * 64, R * 7168 * 4,
-             64 + 128 * ((T + 255) // 256)]
+             64 + 128 * ((T + 63) // 64)]
     assert off[0] == 0
     for b in range(capi.WS_NBUF):
         assert off[b] % 256 == 0

@@ -117,12 +117,15 @@ def test_local_dispatch_invariants(inputs_mod, offset, e_local):
     le = r["ids"] - offset
     local = (le >= 0) & (le < e_local)
     assert d["counts"].sum() == local.sum() == d["offsets"][-1]
+    tok = d["route_token"] & 0x7FFFFFFF
+    single = d["route_token"] < 0  # bit 31: the token's only local route
     for e in range(e_local):
-        rows = d["route_token"][d["offsets"][e]:d["offsets"][e + 1]]
+        rows = tok[d["offsets"][e]:d["offsets"][e + 1]]
         assert (np.diff(rows) > 0).all()  # token order
         assert set(rows.tolist()) == set(np.nonzero((le == e).any(1))[0].tolist())
     for t in range(r["ids"].shape[0]):
         rr = d["token_route"][t]
         n = int(local[t].sum())
         assert (rr[n:] == -1).all() and (rr[:n] >= 0).all() and (np.diff(rr[:n]) > 0).all()
-        assert (d["route_token"][rr[:n]] == t).all()
+        assert (tok[rr[:n]] == t).all()
+        assert (single[rr[:n]] == (n == 1)).all()
