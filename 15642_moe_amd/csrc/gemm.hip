@@ -34,37 +34,6 @@ namespace moe {
 // exit at once.
 // ---------------------------------------------------------------------------
 
-typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v8i frag(const u32x4& lo, const u32x4& hi) {
-  return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-// Loads of the decode K loops are issued from inline assembly (SGPR base +
-// per-lane 32-bit offset, no address arithmetic per K-block) and waited for
-// explicitly: the ring keeps NR-1 K-blocks in flight, one
-// `s_waitcnt vmcnt((NR-1) * loads-per-K-block)` before each K-block's MFMAs,
-// whereas the compiler's own count at the unrolled loop's entry collapses
-// the ring for one K-block in NR.  The registers of the K-block then pass
-// through an empty asm, which orders every use after the wait.  Uniform
-// values (weight-block scales) are loaded the same way rather than by scalar
-// loads, whose waits would cover every outstanding load.
-__device__ __forceinline__ void gload2(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
-  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:1024"
-                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
-}
-__device__ __forceinline__ void gload2_adj(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
-  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
-                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
-}
-__device__ __forceinline__ void gload1(float& x, uint32_t voff, const void* sbase) {
-  __asm__ volatile("global_load_dword %0, %1, %2" : "=&v"(x) : "v"(voff), "s"(sbase) : "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
 __device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice) {
   e = p / nslice;
   slice = p - e * nslice;

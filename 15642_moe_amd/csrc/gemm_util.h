@@ -14,6 +14,56 @@ __device__ __forceinline__ v8i make_v8i(const uint4& lo, const uint4& hi) {
   return r;
 }
 
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v8i frag(const u32x4& lo, const u32x4& hi) {
+  return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Loads of the decode and prefill K loops are issued from inline assembly
+// (SGPR base + per-lane 32-bit offset, no address arithmetic per K-block)
+// and waited for explicitly: a ring keeps several K-blocks in flight, with
+// one `s_waitcnt vmcnt(N)` before each use, N the number of loads issued
+// after the ones it needs, whereas the compiler's own count at the unrolled
+// loop's entry collapses the ring for one K-block in each pass.  The
+// registers of the K-block then pass through an empty asm (settle), which
+// orders every use after the wait.  Uniform values (weight-block scales) are
+// loaded the same way rather than by scalar loads, whose waits would cover
+// every outstanding load.
+__device__ __forceinline__ void gload2(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:1024"
+                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gload2_adj(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:16"
+                   : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gload1(float& x, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dword %0, %1, %2" : "=&v"(x) : "v"(voff), "s"(sbase) : "memory");
+}
+__device__ __forceinline__ void gload_x4(u32x4& d, uint32_t voff, const void* sbase) {
+  __asm__ volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(sbase) : "memory");
+}
+// The 32x32x64 A operand of one K-block from a packed 16x16x128 tile pair:
+// K half kh, 16-byte half h of this lane's fragment at kh*512 + h*1024.
+// r[2kh] / r[2kh+1] are the two halves of K half kh.
+__device__ __forceinline__ void gload_kblock(u32x4 (&r)[4], uint32_t voff, const void* sbase) {
+  __asm__ volatile(
+      "global_load_dwordx4 %0, %4, %5\n\t"
+      "global_load_dwordx4 %1, %4, %5 offset:1024\n\t"
+      "global_load_dwordx4 %2, %4, %5 offset:512\n\t"
+      "global_load_dwordx4 %3, %4, %5 offset:1536"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(voff), "s"(sbase)
+      : "memory");
+}
+__device__ __forceinline__ void settle(u32x4& v) { __asm__ volatile("" : "+v"(v)); }
+__device__ __forceinline__ void settle(float& v) { __asm__ volatile("" : "+v"(v)); }
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 // 32-byte operand fragment of one 2 KB tile in split-half layout:
 // half h of lane l at h*1024 + l*16 (global or LDS).
 __device__ __forceinline__ v8i load_tile_frag(const uint8_t* __restrict__ tile, int lane) {

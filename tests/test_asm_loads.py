@@ -7,9 +7,11 @@ load's destination before its wait (a copy to another register, a spill, a
 reuse for another value), the late load data would land in a register that
 now holds something else.  This test compiles every source of the library
 for gfx950, finds each kernel whose body holds a vector load between
-;;#ASMSTART and ;;#ASMEND, and scans it: between such a load and the
-`s_waitcnt vmcnt` that retires it, no other instruction may read or write the
-load's destination registers.
+;;#ASMSTART and ;;#ASMEND, and checks it: on every path through the
+kernel's control flow (branches and loop back-edges, whatever order the
+compiler lays the blocks out in), between such a load and the
+`s_waitcnt vmcnt` that retires it, no other instruction may read or write
+the load's destination registers.
 """
 
 from __future__ import annotations
@@ -42,14 +44,16 @@ def _regs(text: str) -> set[tuple[str, int]]:
     return out
 
 
-def check_kernel(lines: list[str]) -> list[str]:
-    """Linear scan over one kernel.  Every vector-memory instruction takes a
-    place in the in-order vmcnt queue; `s_waitcnt vmcnt(N)` retires all but
-    the N most recent.  The destinations of loads issued from inline assembly
-    (between ;;#ASMSTART and ;;#ASMEND) are protected until retired: any other
-    instruction that names one of those registers is reported."""
-    queue: list[tuple[int, set]] = []  # (line index, protected registers) in issue order
-    problems = []
+LABEL_RE = re.compile(r"^(\.LBB\w+):")
+BRANCH_RE = re.compile(r"^(s_branch|s_cbranch_\w+)\s+(\.LBB\w+)")
+END_RE = re.compile(r"^(s_endpgm|s_setpc_b64|s_trap)\b")
+WAIT_RE = re.compile(r"s_waitcnt\b.*vmcnt\((\d+)\)")
+MAX_QUEUE = 72  # vmcnt counts to 63; older entries fold into the last position
+
+
+def _instructions(lines: list[str]):
+    """(line index, instruction text, inside inline asm, label) per line that
+    holds an instruction or a label."""
     in_asm = False
     for i, raw in enumerate(lines):
         if ";;#ASMSTART" in raw:
@@ -57,22 +61,112 @@ def check_kernel(lines: list[str]) -> list[str]:
         if ";;#ASMEND" in raw:
             in_asm = False
         ins = raw.split(";")[0].strip()
+        m = LABEL_RE.match(ins)
+        if m:
+            yield i, "", in_asm, m.group(1)
+            continue
         if not ins or ins.endswith(":") or ins.startswith("."):
             continue
-        m = re.match(r"s_waitcnt\b.*vmcnt\((\d+)\)", ins)
+        yield i, ins, in_asm, None
+
+
+def _blocks(lines: list[str]):
+    """Basic blocks of one kernel body: a list of (instructions, successor
+    block indices), instructions as (line index, text, inside inline asm)."""
+    blocks, labels = [], {}
+    cur: list = []
+    term: list = []  # per block: (branch target label or None, falls through)
+
+    def close(target, falls):
+        blocks.append(cur)
+        term.append((target, falls))
+
+    for i, ins, in_asm, label in _instructions(lines):
+        if label is not None:
+            if cur:
+                close(None, True)
+                cur = []
+            labels[label] = len(blocks)
+            continue
+        cur.append((i, ins, in_asm))
+        b = BRANCH_RE.match(ins)
+        if b:
+            close(b.group(2), b.group(1) != "s_branch")
+            cur = []
+        elif END_RE.match(ins):
+            close(None, False)
+            cur = []
+    if cur:
+        close(None, False)
+    succ = []
+    for k, (target, falls) in enumerate(term):
+        s = []
+        if target is not None and target in labels:
+            s.append(labels[target])
+        if falls and k + 1 < len(blocks):
+            s.append(k + 1)
+        succ.append(s)
+    return list(zip(blocks, succ))
+
+
+def _merge(a: tuple, b: tuple) -> tuple:
+    n = max(len(a), len(b))
+    return tuple((a[k] if k < len(a) else frozenset()) | (b[k] if k < len(b) else frozenset()) for k in range(n))
+
+
+def _transfer(state: tuple, block, problems=None) -> tuple:
+    """The vmcnt queue after one block.  state[k] is the set of registers
+    protected by the k-th youngest outstanding vector-memory instruction
+    (over every path that reaches the block, so a register is flagged if any
+    path may still be loading it)."""
+    for i, ins, in_asm in block:
+        m = WAIT_RE.match(ins)
         if m:
-            n = int(m.group(1))
-            queue = queue[len(queue) - n:] if n < len(queue) else queue
+            state = state[:int(m.group(1))]
             continue
         if ins.startswith("s_waitcnt"):
             continue
-        lm = LOAD_RE.match(ins)
-        touched = _regs(ins)
-        for j, d in queue:
-            if d & touched:
-                problems.append(f"line {i}: {ins} touches registers of the load at line {j}: {lines[j].strip()}")
+        if problems is not None:
+            touched = _regs(ins)
+            for k, d in enumerate(state):
+                if d & touched:
+                    problems.append(f"line {i}: {ins} touches registers of a load still in flight "
+                                    f"({k} younger vector-memory instructions)")
         if VMEM_RE.match(ins):
-            queue.append((i, _regs(lm.group(2)) if (lm and in_asm) else set()))
+            lm = LOAD_RE.match(ins)
+            state = (frozenset(_regs(lm.group(2))) if (lm and in_asm) else frozenset(),) + state
+            if len(state) > MAX_QUEUE:
+                state = state[:MAX_QUEUE - 1] + (frozenset().union(*state[MAX_QUEUE - 1:]),)
+    return state
+
+
+def check_kernel(lines: list[str]) -> list[str]:
+    """Dataflow over the kernel's basic blocks.  Every vector-memory
+    instruction takes a place in the in-order vmcnt queue; `s_waitcnt
+    vmcnt(N)` retires all but the N most recent.  The destinations of loads
+    issued from inline assembly (between ;;#ASMSTART and ;;#ASMEND) are
+    protected until retired: any other instruction that names one of those
+    registers on some path is reported.  Queue states meeting at a block are
+    merged position by position (k-th youngest with k-th youngest), which
+    over-approximates every path, loops included (iterated to a fixpoint)."""
+    blocks = _blocks(lines)
+    if not blocks:
+        return []
+    state_in = [None] * len(blocks)
+    state_in[0] = ()
+    work = [0]
+    while work:
+        k = work.pop()
+        out = _transfer(state_in[k], blocks[k][0])
+        for s in blocks[k][1]:
+            new = out if state_in[s] is None else _merge(state_in[s], out)
+            if new != state_in[s]:
+                state_in[s] = new
+                work.append(s)
+    problems: list[str] = []
+    for k, (block, _) in enumerate(blocks):
+        if state_in[k] is not None:
+            _transfer(state_in[k], block, problems)
     return problems
 
 
@@ -151,3 +245,25 @@ def test_checker_flags_a_moved_destination():
     # does not select one, an asm load under any kernel name does
     assert has_asm_load(bad) and has_asm_load(good)
     assert not has_asm_load(["global_load_dwordx4 v[0:3], v248, s[16:17]", "s_waitcnt vmcnt(0)"])
+
+
+def test_checker_follows_control_flow():
+    """Hazards that only a path through a branch or a loop back-edge shows
+    are flagged; a safe loop whose latch block is laid out before its header
+    is not."""
+    load = [";;#ASMSTART", "global_load_dwordx4 v[0:3], v248, s[16:17]", ";;#ASMEND"]
+    # back-edge: the load at the loop bottom, its register read at the top
+    loop = [".LBB0_1:", "v_add_u32_e32 v5, v0, v5", *load, "s_cbranch_scc1 .LBB0_1", "s_endpgm"]
+    assert check_kernel(loop)
+    # the same loop waiting at the top is fine
+    loop_ok = [".LBB0_1:", "s_waitcnt vmcnt(0)", "v_add_u32_e32 v5, v0, v5", *load,
+               "s_cbranch_scc1 .LBB0_1", "s_waitcnt vmcnt(0)", "s_endpgm"]
+    assert not check_kernel(loop_ok)
+    # one path skips the wait
+    branch = [*load, "s_cbranch_scc0 .LBB0_2", "s_waitcnt vmcnt(0)", ".LBB0_2:", "v_mov_b32_e32 v9, v1"]
+    assert check_kernel(branch)
+    # latch laid out before the header (entry branches over it): the wait in
+    # the header runs before the use in the latch on every path
+    rotated = [*load, "s_branch .LBB0_3", ".LBB0_2:", "v_mov_b32_e32 v9, v1", *load,
+               ".LBB0_3:", "s_waitcnt vmcnt(0)", "s_cbranch_scc1 .LBB0_2", "s_endpgm"]
+    assert not check_kernel(rotated)
