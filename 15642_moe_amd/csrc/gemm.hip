@@ -48,14 +48,15 @@ __device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice
 // with wave ballots (counts, offsets, its expert's tokens in token order);
 // items j == 0 publish their expert's route arrays, item (0, 0) the counts,
 // offsets and the -1 tails of token_route.
-template <int NR, int FR>
+template <int NR, int FR, int NPW>
 __global__ void __launch_bounds__(64)
 stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
                      int offset, const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
                      const uint8_t* __restrict__ w13p, const float* __restrict__ w13s, int32_t* __restrict__ counts,
                      int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
                      float* __restrict__ route_weight, int32_t* __restrict__ token_route, float* __restrict__ Cf) {
-  constexpr int BM = 16, NPW = 2, NPAIR = I / 16 / NPW;
+  constexpr int BM = 16, NPAIR = I / 16 / NPW;
+  static_assert(8 % NPW == 0, "an item's tile pairs lie in one 128-column block");
   static_assert(HB % NR == 0, "ring depth must divide the K-block count");
   __shared__ int s_tok[DECODE_MAX_T];
   const int lane = threadIdx.x;
@@ -375,17 +376,18 @@ hipError_t launch_stage1_decode(const int32_t* topk_ids, const float* topk_w, in
                                 float* route_weight, int32_t* token_route, float* Cf, uint8_t* Cq, float* Cs,
                                 hipStream_t stream) {
   if (T > DECODE_MAX_T) return hipErrorInvalidValue;
-  const int grid = e_local * (I / 32);
+  constexpr int NPW = 2;
+  const int grid = e_local * (I / 16 / NPW);
   // Two fragments per weight pass once experts can hold more than 16
   // routes often enough to matter; at T <= 64 one (its registers keep two
   // waves per SIMD either way, but the second fragment's loads would be
   // padding for nearly every item).
   if (T > 64)
-    stage1_decode_kernel<4, 2><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
+    stage1_decode_kernel<4, 2, NPW><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
                                                         w13p, w13_scale, counts, offsets, route_token, route_weight,
                                                         token_route, Cf);
   else
-    stage1_decode_kernel<4, 1><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
+    stage1_decode_kernel<4, 1, NPW><<<grid, 64, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, hidden, hidden_scale,
                                                         w13p, w13_scale, counts, offsets, route_token, route_weight,
                                                         token_route, Cf);
   hipError_t err = hipGetLastError();

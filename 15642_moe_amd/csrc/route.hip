@@ -35,11 +35,8 @@ __device__ __forceinline__ int popc(uint64_t m) { return __popcll(m); }
 
 // Cross-lane moves by DPP (no LDS round trip): quad_perm [1,0,3,2] and
 // [2,3,0,1] pair lanes l ^ 1 and l ^ 2, row_half_mirror l ^ 7 within 8
-// lanes, row_mirror l ^ 15 within a 16-lane row; row_bcast:15 / :31 copy
-// the last lane of the row below into rows 1, 3 / 2, 3 (lanes outside the
-// row mask keep their own value).
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
-constexpr int DPP_BCAST15 = 0x142, DPP_BCAST31 = 0x143;
+// lanes.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141;
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROW_MASK, 0xF, false);
@@ -47,17 +44,6 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
   return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(x)));
-}
-
-// Maximum over the wave's 64 lanes (wave-uniform result).
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
-  x = max(x, dpp_u32<DPP_XOR1>(x));
-  x = max(x, dpp_u32<DPP_XOR2>(x));
-  x = max(x, dpp_u32<DPP_HALF_MIRROR>(x));
-  x = max(x, dpp_u32<DPP_MIRROR>(x));            // every lane of a row: the row's max
-  x = max(x, dpp_u32<DPP_BCAST15, 0xA>(x));      // rows 1, 3: max of rows 0-1, 2-3
-  x = max(x, dpp_u32<DPP_BCAST31, 0xC>(x));      // row 3: max of rows 0-3
-  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
 }
 
 __global__ void __launch_bounds__(256)
@@ -106,28 +92,36 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   }
   const bool group_sel = rank < TOPK_GROUP;
 
-  // Top-8 experts of the kept groups by (value desc, index asc): eight
-  // rounds of a wave-wide max of the lanes' best remaining key; ties at the
-  // maximum go to the lowest lane (lowest experts), and within that lane to
-  // its lowest expert.  The picked key is cleared for the next round.
+  // Top-8 experts of the kept groups by (value desc, index asc): the 8th
+  // largest key is found bit by bit from wave-wide ballot counts (scalar
+  // popcounts, so the loop is mostly SALU work beside four compares), then
+  // ties at that key are filled in ascending expert order.
   uint32_t key[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) key[j] = group_sel ? order_key(v[j]) : 0u;
-  bool sel[4] = {false, false, false, false};
-#pragma unroll 1
-  for (int k = 0; k < TOP_K; ++k) {
-    const uint32_t lk = max(max(key[0], key[1]), max(key[2], key[3]));
-    const uint32_t M = wave_max_u32(lk);
-    const uint64_t bal = __ballot(lk == M);
-    const int win = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(bal));
-    if (lane == win) {
-      const int j = key[0] == M ? 0 : key[1] == M ? 1 : key[2] == M ? 2 : 3;
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int cnt = 0;
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        if (jj == j) { sel[jj] = true; key[jj] = 0u; }
-    }
+    for (int j = 0; j < 4; ++j) cnt += popc(__ballot(key[j] >= cand));
+    if (cnt >= TOP_K) thr = cand;
   }
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int n_gt = 0, eq_seen = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    n_gt += popc(__ballot(key[j] > thr));
+    eq_seen += popc(__ballot(key[j] == thr) & below);
+  }
+  const int need = TOP_K - n_gt;
+  bool sel[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool eq = key[j] == thr;
+    sel[j] = key[j] > thr || (eq && eq_seen < need);
+    eq_seen += eq ? 1 : 0;
+  }
   // Position in ascending expert order = selected experts below this one.
   int pos = 0;
 #pragma unroll
