@@ -13,6 +13,9 @@ H_BLOCKS = H // BLOCK            # 56
 I_BLOCKS = I_DIM // BLOCK        # 16
 G1_BLOCKS = 2 * I_DIM // BLOCK   # 32
 MAX_E_LOCAL = 32
+# Largest T served by the decode (weight-streaming) GEMMs; above it the
+# prefill tile kernels run (csrc/common.h DECODE_MAX_T).
+DECODE_MAX_T = 128
 
 # Packed operand layouts (int32 views, 16 bytes per lane half):
 #   W13: [E, nb=16, kb=56, tile=16, half=2, lane=64, 4]

@@ -2,6 +2,7 @@
 """moe_forward benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4] [--no-cpu-baseline]
+                    [--no-headline] [--no-upstream]
 
 A step is one moe_forward (route, dispatch, GEMM1+SwiGLU+FP8 requant,
 GEMM2, combine) over one batch with pre-packed weights already resident in
@@ -9,14 +10,19 @@ HBM; the one-time pack is timed separately.  The headline line is the decode
 configuration (T=64); the other configurations are timed
 too and reported under "configs".  Per-kernel durations come from HIP events
 recorded on the launch stream between the kernels (moe_forward_timed), and
-give the roofline figure of the dominant kernel.  The CPU baseline times the
-oracle's restatement of reference/moe_ref.py (full fp32 dequant, per-expert
-fp32 GEMMs) on the host, on one forward of the same decode batch.  Under
+give the roofline figure of the dominant kernel.  Each configuration is also
+timed through moe_layer.run_custom, the drop-in path the reference's own
+benchmark times (pack-cache lookups, fp32 casts, then ops.moe_forward).  The
+CPU baseline times the oracle's restatement of reference/moe_ref.py (full
+fp32 dequant, per-expert fp32 GEMMs) on the host, on whole forwards of each
+configuration's batch (a bounded number per configuration).  Under
 "upstream", the producer of the forward's inputs (moe_router_quant: router
 GEMM + dynamic FP8 activation quantisation from bf16 hidden states) is timed
 at each configuration's T.
 
-Prints one JSON line on stdout; progress goes to stderr.
+Prints one JSON line on stdout; progress goes to stderr.  --no-headline
+times only the listed configurations (for per-configuration kernel traces)
+and prints a line with their records only.
 """
 
 from __future__ import annotations
@@ -43,17 +49,24 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def _traffic_from_profiles(config_name: str):
-    """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 PMC summary (profiles/<kernel>_<workload>_traffic.txt, a line
-    'traffic_bytes_per_launch: N'), or None."""
-    p = REPO / "profiles" / f"stage1_{config_name}_traffic.txt"
+def _traffic_from_profiles(config_name: str) -> dict:
+    """HBM bytes per launch of the dominant kernel, the kernel and the commit
+    it was measured at, from the committed rocprofv3 PMC summary
+    (profiles/traffic_<workload>.txt: 'traffic_bytes_per_launch: N',
+    'dominant_kernel: ...', 'commit: ...'); values None when absent."""
+    rec = {"traffic": None, "traffic_kernel": None, "traffic_commit": None}
+    p = REPO / "profiles" / f"traffic_{config_name}.txt"
     if not p.exists():
-        return None
+        return rec
     for line in p.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        key, _, val = line.partition(":")
+        if key == "traffic_bytes_per_launch":
+            rec["traffic"] = float(val)
+        elif key == "dominant_kernel":
+            rec["traffic_kernel"] = val.strip()
+        elif key == "commit":
+            rec["traffic_commit"] = val.strip()
+    return rec
 
 
 def main() -> int:
@@ -63,7 +76,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--configs", default="1,2,3,4", help="benchmark configs to time (headline: 1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget-s", type=float, default=25.0)
+    ap.add_argument("--cpu-budget-s", type=float, default=12.0, help="CPU-baseline wall time per configuration")
+    ap.add_argument("--no-headline", action="store_true",
+                    help="time only the listed configs (no headline config 1, no summary line)")
+    ap.add_argument("--no-upstream", action="store_true", help="skip the moe_router_quant timing")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run one plain 512 MiB device copy (the known-size reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes) and exit")
@@ -90,10 +106,11 @@ def main() -> int:
     torch.cuda.set_device(dev)
 
     cfg_ids = [int(c) for c in args.configs.split(",") if c.strip()]
-    if 1 not in cfg_ids:
+    if 1 not in cfg_ids and not args.no_headline:
         cfg_ids = [1] + cfg_ids
+    moe_layer = importlib.import_module("15642_moe_amd.moe_layer")
     results = {}
-    headline_inputs_cpu = None
+    cpu_runs = {}
 
     for idx in cfg_ids:
         cfg = inputs_mod.CONFIGS[idx]
@@ -168,11 +185,32 @@ def main() -> int:
         stage_us = {}
         for i, name in enumerate(STAGES):
             stage_us[name] = sum(row[i].elapsed_time(row[i + 1]) for row in evs) * 1e3 / args.steps
+        if T <= geo.DECODE_MAX_T:
+            # the decode path runs its dispatch inside GEMM1: the event pair
+            # around the dispatch stage brackets no kernel (only event cost)
+            stage_us["dispatch"] = None
+
+        # the drop-in path the reference benchmark times: moe_layer.run_custom
+        # (its pack cache is filled by the warm-up calls)
+        kw = {k: inp[k] for k in ("routing_logits", "routing_bias", "hidden_states", "hidden_states_scale",
+                                  "gemm1_weights", "gemm1_weights_scale", "gemm2_weights", "gemm2_weights_scale")}
+        kw.update(local_expert_offset=off, routed_scaling_factor=rsf)
+        for _ in range(max(args.warmup, 1)):
+            moe_layer.run_custom(ops, **kw)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(args.steps):
+            moe_layer.run_custom(ops, **kw)
+        end.record(stream)
+        torch.cuda.synchronize()
+        run_custom_us = start.elapsed_time(end) * 1e3 / args.steps
+        moe_layer._packed_weight_cache.clear()
 
         rec = {
             "T": T,
             "local_expert_offset": off,
             "latency_us": round(lat_us, 2),
+            "run_custom_us": round(run_custom_us, 2),
             "local_routes": routes,
             "hit_experts": hit,
             "alg_bytes": alg_bytes,
@@ -180,7 +218,7 @@ def main() -> int:
             "hbm_gbs": round(alg_bytes / (lat_us * 1e-6) / 1e9, 1),
             "hbm_frac": round(alg_bytes / (lat_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "mfma_util": round(alg_flops / (lat_us * 1e-6) / 1e12 / FP8_PEAK_TFLOPS, 4),
-            "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+            "stage_us": {k: (None if v is None else round(v, 2)) for k, v in stage_us.items()},
             "stage_gbs": {k: round(stage_bytes[k] / (stage_us[k] * 1e-6) / 1e9, 1) for k in stage_bytes},
             "stage_tflops": {k: round(stage_flops[k] / (stage_us[k] * 1e-6) / 1e12, 2) for k in stage_flops},
             "stage_alg_bytes": stage_bytes,
@@ -188,12 +226,19 @@ def main() -> int:
         }
         results[cfg.name] = rec
         log(f"config {idx}: {json.dumps(rec)}")
-        if idx == 1 and not args.no_cpu_baseline:
-            headline_inputs_cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
-        del inp, p13, p2, args_fwd, out, ws, evs
+        if not args.no_cpu_baseline:
+            cpu_runs[cfg.name] = _cpu_baseline(
+                {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}, cfg, lat_us,
+                args.cpu_budget_s)
+        del inp, p13, p2, args_fwd, out, ws, evs, kw
         torch.cuda.empty_cache()
 
-    upstream = [_time_upstream(torch, lib, dev, inputs_mod.CONFIGS[i].T, args.steps) for i in cfg_ids]
+    if args.no_headline:
+        print(json.dumps({"metric": METRIC, "configs": results, "cpu_baseline_per_config": cpu_runs or None}),
+              flush=True)
+        return 0
+    upstream = [] if args.no_upstream else [
+        _time_upstream(torch, lib, dev, inputs_mod.CONFIGS[i].T, args.steps) for i in cfg_ids]
 
     head = results[inputs_mod.CONFIGS[1].name]
     dom = max(("gemm1_swiglu_quant", "gemm2"), key=lambda k: head["stage_us"][k])
@@ -205,40 +250,24 @@ def main() -> int:
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": _traffic_from_profiles(inputs_mod.CONFIGS[1].name),
+        **_traffic_from_profiles(inputs_mod.CONFIGS[1].name),
         "launch_us": head["stage_us"][dom],
         "alg_bytes_per_launch": head["stage_alg_bytes"][dom],
     }
 
     cpu_baseline = None
-    if not args.no_cpu_baseline and headline_inputs_cpu is not None:
-        import torch as _t
-
-        from oracle import moe_cpu  # CPU-baseline leg only
-
-        cores = len(os.sched_getaffinity(0))
-        _t.set_num_threads(cores)
-        log(f"cpu baseline: oracle restatement of moe_ref.run, T=64, {cores} threads")
-        times = []
-        t_budget = time.perf_counter() + args.cpu_budget_s
-        while True:
-            t0 = time.perf_counter()
-            moe_cpu.forward_full_dequant(headline_inputs_cpu)
-            times.append(time.perf_counter() - t0)
-            log(f"cpu baseline forward {len(times)}: {times[-1]:.2f} s")
-            if len(times) >= 3 or time.perf_counter() + times[-1] > t_budget:
-                break
-        steady = times[1:] if len(times) > 1 else times
-        cpu_us = sum(steady) / len(steady) * 1e6
+    hname = inputs_mod.CONFIGS[1].name
+    if hname in cpu_runs:
+        c = cpu_runs[hname]
         cpu_baseline = {
-            "value": round(cpu_us, 1),
+            "value": c["us"],
             "unit": "us per moe_forward (T=64)",
-            "cores": _t.get_num_threads(),
+            "cores": c["cores"],
             "kind": "port",
-            "sample": f"{len(times)} full forwards of the decode batch (T=64, config 1), first treated as warm-up"
-                      if len(times) > 1 else "1 full forward of the decode batch (T=64, config 1)",
+            "sample": c["sample"],
             "cpu": _cpu_model(),
-            "gpu_speedup": round(cpu_us / head["latency_us"], 1),
+            "gpu_speedup": c["gpu_speedup"],
+            "per_config": cpu_runs,
         }
 
     line = {
@@ -271,6 +300,39 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _cpu_baseline(inputs_cpu: dict, cfg, gpu_us: float, budget_s: float) -> dict:
+    """The oracle's restatement of reference/moe_ref.run (full fp32 dequant,
+    per-expert fp32 GEMMs) on whole forwards of one configuration's batch, on
+    the host's cores: up to three forwards, or fewer when the next would run
+    past budget_s; the first is a warm-up when there are several."""
+    import torch
+
+    from oracle import moe_cpu  # CPU-baseline leg only
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    log(f"cpu baseline: oracle restatement of moe_ref.run, {cfg.name} (T={cfg.T}), {cores} threads")
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while True:
+        t0 = time.perf_counter()
+        moe_cpu.forward_full_dequant(inputs_cpu)
+        times.append(time.perf_counter() - t0)
+        log(f"cpu baseline {cfg.name} forward {len(times)}: {times[-1]:.2f} s")
+        if len(times) >= 3 or time.perf_counter() + times[-1] > t_end:
+            break
+    steady = times[1:] if len(times) > 1 else times
+    us = sum(steady) / len(steady) * 1e6
+    return {
+        "us": round(us, 1),
+        "T": cfg.T,
+        "cores": torch.get_num_threads(),
+        "sample": (f"{len(times)} full forwards of config {cfg.name}, first treated as warm-up" if len(times) > 1
+                   else f"1 full forward of config {cfg.name}"),
+        "gpu_speedup": round(us / gpu_us, 1),
+    }
 
 
 def _time_upstream(torch, lib, dev, T: int, steps: int) -> dict:

@@ -144,3 +144,15 @@ def test_config_inputs_cpu_shapes(inputs_mod):
     w13, w2 = inputs_mod.expert_weights_host(inputs_mod.CONFIGS[0], [3, 17])
     assert np.array_equal(w13[0], inp["gemm1_weights"][3].view(torch.uint8).numpy())
     assert np.array_equal(w2[1], inp["gemm2_weights"][17].view(torch.uint8).numpy())
+
+
+def test_geometry_matches_kernel_constants():
+    """The host constants bench.py and the tests use agree with the kernels'."""
+    import re
+    from pathlib import Path
+
+    geo = pkg("geometry")
+    common = (Path(__file__).resolve().parents[1] / "15642_moe_amd" / "csrc" / "common.h").read_text()
+    for name, value in (("DECODE_MAX_T", geo.DECODE_MAX_T), ("MAX_E_LOCAL", geo.MAX_E_LOCAL)):
+        m = re.search(rf"constexpr int {name} = (\d+);", common)
+        assert m and int(m.group(1)) == value, name
