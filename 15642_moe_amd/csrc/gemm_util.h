@@ -20,16 +20,16 @@ __device__ __forceinline__ v8i frag(const u32x4& lo, const u32x4& hi) {
   return __builtin_bit_cast(v8i, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// Loads of the decode and prefill K loops are issued from inline assembly
-// (SGPR base + per-lane 32-bit offset, no address arithmetic per K-block)
-// and waited for explicitly: a ring keeps several K-blocks in flight, with
-// one `s_waitcnt vmcnt(N)` before each use, N the number of loads issued
-// after the ones it needs, whereas the compiler's own count at the unrolled
-// loop's entry collapses the ring for one K-block in each pass.  The
-// registers of the K-block then pass through an empty asm (settle), which
-// orders every use after the wait.  Uniform values (weight-block scales) are
-// loaded the same way rather than by scalar loads, whose waits would cover
-// every outstanding load.
+// Loads of the decode K loops are issued from inline assembly (SGPR base +
+// per-lane 32-bit offset, no address arithmetic per K-block) and waited for
+// explicitly: a ring keeps several K-blocks in flight, with one
+// `s_waitcnt vmcnt(N)` before each use, N the number of loads issued after
+// the ones it needs, whereas the compiler's own count at the unrolled loop's
+// entry collapses the ring for one K-block in each pass.  The registers of
+// the K-block then pass through an empty asm, which orders every use after
+// the wait.  Uniform values (weight-block scales) are loaded the same way
+// rather than by scalar loads, whose waits would cover every outstanding
+// load.
 __device__ __forceinline__ void gload2(u32x4& lo, u32x4& hi, uint32_t voff, const void* sbase) {
   __asm__ volatile("global_load_dwordx4 %0, %2, %3\n\tglobal_load_dwordx4 %1, %2, %3 offset:1024"
                    : "=&v"(lo), "=&v"(hi) : "v"(voff), "s"(sbase) : "memory");
@@ -41,24 +41,6 @@ __device__ __forceinline__ void gload2_adj(u32x4& lo, u32x4& hi, uint32_t voff, 
 __device__ __forceinline__ void gload1(float& x, uint32_t voff, const void* sbase) {
   __asm__ volatile("global_load_dword %0, %1, %2" : "=&v"(x) : "v"(voff), "s"(sbase) : "memory");
 }
-__device__ __forceinline__ void gload_x4(u32x4& d, uint32_t voff, const void* sbase) {
-  __asm__ volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(sbase) : "memory");
-}
-// The 32x32x64 A operand of one K-block from a packed 16x16x128 tile pair:
-// K half kh, 16-byte half h of this lane's fragment at kh*512 + h*1024.
-// r[2kh] / r[2kh+1] are the two halves of K half kh.
-__device__ __forceinline__ void gload_kblock(u32x4 (&r)[4], uint32_t voff, const void* sbase) {
-  __asm__ volatile(
-      "global_load_dwordx4 %0, %4, %5\n\t"
-      "global_load_dwordx4 %1, %4, %5 offset:1024\n\t"
-      "global_load_dwordx4 %2, %4, %5 offset:512\n\t"
-      "global_load_dwordx4 %3, %4, %5 offset:1536"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-      : "v"(voff), "s"(sbase)
-      : "memory");
-}
-__device__ __forceinline__ void settle(u32x4& v) { __asm__ volatile("" : "+v"(v)); }
-__device__ __forceinline__ void settle(float& v) { __asm__ volatile("" : "+v"(v)); }
 template <int N>
 __device__ __forceinline__ void wait_vm() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
@@ -93,14 +75,26 @@ __device__ __forceinline__ void load_tile_table(const int32_t* __restrict__ coun
 }
 
 // Logical work L -> (expert, weight block, route tile).  Works are ordered
-// expert-major, then weight block, then route tile: the route tiles that
-// read one weight block are neighbours, so a contiguous run of works on one
-// XCD fetches each weight K-block into that XCD's L2 once for all of them
-// (an expert's route tiles also re-read their activations once per weight
-// block, but a route tile's K-block is smaller than a weight block's).
-// The expert is found by one LDS read per lane and a ballot (lane l tests
-// expert l), not a scan of dependent reads: L < s_tp[e_local] * nblk is a
-// valid work, so exactly one expert's range holds it.
+// expert-major, then (per band of route tiles, below) weight block, then
+// route tile: the route tiles that read one weight block are neighbours, so
+// a contiguous run of works on one XCD fetches each weight K-block into that
+// XCD's L2 once for all of them (the route tiles re-read their activations
+// once per weight block, but a route tile's K-block is smaller than a
+// weight block's).  The expert is found by one LDS read per lane and a
+// ballot (lane l tests expert l), not a scan of dependent reads:
+// L < s_tp[e_local] * nblk is a valid work, so exactly one expert's range
+// holds it.
+//
+// An expert with more than WORK_BAND route tiles is cut into bands of
+// WORK_BAND route tiles (the last band shorter), and its works run band by
+// band, each band over all weight blocks: the works an XCD runs together
+// then share a few weight blocks and a few route tiles' activations,
+// instead of one weight block and every route tile of the expert, whose
+// activations (tens of MB for a heavily routed expert) no L2 keeps from one
+// weight block to the next.  Measured by FETCH_SIZE at skewed T=4096 (four
+// experts of 4096 routes): GEMM1 moved 3.0x its algorithmic bytes in plain
+// (weight block, route tile) order.
+constexpr int WORK_BAND = 8;
 __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const int* s_tp, int& e, int& blk,
                                             int& mt) {
   const int l = threadIdx.x & 63, li = l < e_local ? l : 0;  // every read inside s_tp[0 .. e_local]
@@ -108,8 +102,18 @@ __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const 
   e = __builtin_amdgcn_readfirstlane(__builtin_ctzll(__ballot(mine)));
   const int nt = s_tp[e + 1] - s_tp[e];  // >= 1: L lies inside expert e's works
   const int local = L - s_tp[e] * nblk;
-  blk = local / nt;
-  mt = local - blk * nt;
+  const int full = nt / WORK_BAND;            // whole bands
+  const int band = local / (WORK_BAND * nblk);
+  if (band < full) {
+    const int r = local - band * WORK_BAND * nblk;
+    blk = r / WORK_BAND;
+    mt = band * WORK_BAND + (r - blk * WORK_BAND);
+  } else {  // the last, shorter band (all of an expert with <= WORK_BAND tiles)
+    const int rem = nt - full * WORK_BAND;
+    const int r = local - full * WORK_BAND * nblk;
+    blk = r / rem;
+    mt = full * WORK_BAND + (r - blk * rem);
+  }
 }
 
 // Routes of route tile mt of expert e: [m0, m0 + rows).  The expert's
