@@ -276,7 +276,7 @@ def _largest_expert(idx):
 def test_forward_full_size_expert_routes(ops, inputs_mod, cuda, packed_cache, idx, le):
     """All routes of one expert at full size: the T=8192 expert with the most
     routes, and each of the four experts that every token picks under the
-    skewed routing (4,096 routes, ~22 route tiles each)."""
+    skewed routing (4,096 routes, 32 route tiles of 128 each)."""
     le = _largest_expert(idx) if le == "largest" else le
     print(f"[forward] config {idx}: every route of expert {le}", flush=True)
     inp, p13, p2 = _prepared(idx, inputs_mod, ops, cuda, packed_cache)
