@@ -274,7 +274,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
   }
   MOE_TRY(mark(4));
   MOE_TRY(hip_status(moe::launch_combine(Y, token_route, T, static_cast<uint16_t*>(out_bf16), st),
-                     "combine_kernel launch"));
+                     "combine launch"));
   MOE_TRY(mark(5));
   return MOE_OK;
 }

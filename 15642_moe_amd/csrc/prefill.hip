@@ -51,6 +51,12 @@ constexpr int NWAVES = 8;
 constexpr int RT = 32;                 // routes per route tile
 constexpr int FRAG_BYTES = 4096;       // one route tile's K-block in LDS
 constexpr int NBUF = 2;                // LDS buffers (K-blocks in flight)
+// Epilogue row strides in LDS (bytes / floats): stage 1 stages FP8 rows of
+// 128 bytes, stage 2 fp32 rows of 256 columns; the padding spreads the
+// column-wise writes of 32 routes over the banks, and both stay 16-byte
+// aligned for the row-wise 16-byte reads.
+constexpr int CQ_LDS_STRIDE = BLK + 16;
+constexpr int Y_LDS_STRIDE = 2 * BLK + 4;
 
 // CT route tiles of 32 per item.
 template <int CT>
@@ -319,6 +325,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
   constexpr int BM = G::BM, NSC = 2;
   static_assert(HB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   static_assert(HB <= 64, "one K-block scale per lane");
+  static_assert(BM * CQ_LDS_STRIDE <= CT * NBUF * FRAG_BYTES, "epilogue FP8 rows fit in s_act");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * NBUF * FRAG_BYTES];
   __shared__ float2 s_scl[NBUF * G::NT];
   __shared__ uint32_t s_rowoff[BM], s_soff[BM];
@@ -445,7 +452,11 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         m = fmaxf(m, __shfl_xor(m, 32));
         if (lane < 32) s_red[w][cc * RT + lane] = m;
       }
-      __syncthreads();
+      __syncthreads();  // also: every wave is past its K loop, so s_act is free
+      // The FP8 codes go to LDS first, one 128-byte row per route (this
+      // wave's 16 I columns of it), and leave as whole rows: a store of a
+      // lane's own 4-byte pieces would touch 32 rows (32 cache lines) per
+      // instruction.
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
         const int row = cc * RT + (lane & 31);
@@ -456,7 +467,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
           const float sc = fmaxf(am / E4M3_MAX, 1.0e-8f);
           const float isc = __builtin_amdgcn_rcpf(sc);
           // registers 0-3: I columns 4*(l/32) + 0..3, 4-7: 8 + 4*(l/32) + 0..3
-          uint8_t* crow = Cq + (size_t)(rb + row) * I + nb * BLK + 16 * w + 4 * (lane >> 5);
+          uint8_t* crow = s_act + row * CQ_LDS_STRIDE + 16 * w + 4 * (lane >> 5);
 #pragma unroll
           for (int hq = 0; hq < 2; ++hq) {
             float v[4];
@@ -466,6 +477,12 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
           }
           if (w == 0 && lane < 32) Cs[(size_t)(rb + row) * IB + nb] = sc;
         }
+      }
+      __syncthreads();
+      // Eight threads per row, 16 bytes each.
+      for (int row = tid >> 3; row < rows; row += G::NT / 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(s_act + row * CQ_LDS_STRIDE + 16 * (tid & 7));
+        *reinterpret_cast<uint4*>(Cq + (size_t)(rb + row) * I + nb * BLK + 16 * (tid & 7)) = v;
       }
     });
     __syncthreads();
@@ -488,6 +505,8 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
                    int e_local, int32_t* __restrict__ queue) {
   using G = TileGeom<CT>;
   constexpr int BM = G::BM, NHP = HB / 2, NSC = 1;
+  static_assert(RT * Y_LDS_STRIDE * 4 <= CT * NBUF * FRAG_BYTES, "epilogue fp32 rows of a route tile fit in s_act");
+  static_assert(RT % NWAVES == 0 && 64 * 4 == 2 * BLK, "one 256-column row per wave-wide access");
   static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   static_assert(2 * IB <= 64, "one K-block scale per lane");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * NBUF * FRAG_BYTES];
@@ -595,24 +614,40 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       if (tid == 0) claimed = atomicAdd(&queue[q], 1);
 
       // Lane l holds route cc*32 + l%32 and the wave's H rows 8*j + 4*(l/32)
-      // + 0..3 (registers 4j..4j+3): four float4 pieces per route tile.
-      const size_t hcol = (size_t)hb * BLK + 16 * t0 + 4 * (lane >> 5);
+      // + 0..3 (registers 4j..4j+3), i.e. the item's output columns 32w +
+      // 8j + 4*(l/32) + 0..3 (H column 256*hp + that).  One route tile at a
+      // time goes through LDS and leaves as whole 1 KB rows (Y) or 512-byte
+      // rows (bf16 output of a single-route token), one row per store
+      // instruction: a lane's own float4 pieces would touch 32 rows per
+      // instruction.
+      __syncthreads();  // every wave is past its K loop, so s_act is free
+      float* s_y = reinterpret_cast<float*>(s_act);
+      const size_t hcol = (size_t)hp * (2 * BLK) + 4 * lane;
 #pragma unroll
       for (int cc = 0; cc < NC; ++cc) {
-        const int row = cc * RT + (lane & 31);
-        if (row < rows) {
-          const float rw = s_rw[row];
-          const int tk = s_single[row];
+        {
+          const int rt = lane & 31;
+          const float rw = s_rw[cc * RT + rt];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float4 v = make_float4(acc[cc][4 * j] * rw, acc[cc][4 * j + 1] * rw, acc[cc][4 * j + 2] * rw,
-                                         acc[cc][4 * j + 3] * rw);
+          for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<float4*>(s_y + rt * Y_LDS_STRIDE + 32 * w + 8 * j + 4 * (lane >> 5)) =
+                make_float4(acc[cc][4 * j] * rw, acc[cc][4 * j + 1] * rw, acc[cc][4 * j + 2] * rw,
+                            acc[cc][4 * j + 3] * rw);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < RT / NWAVES; ++k) {
+          const int rt = w + NWAVES * k, row = cc * RT + rt;
+          if (row < rows) {
+            const float4 v = *reinterpret_cast<const float4*>(s_y + rt * Y_LDS_STRIDE + 4 * lane);
+            const int tk = s_single[row];
             if (tk >= 0)
-              store_out_bf16x4(out + (size_t)tk * H + hcol + 8 * j, v);
+              store_out_bf16x4(out + (size_t)tk * H + hcol, v);
             else
-              *reinterpret_cast<float4*>(Y + (size_t)(rb + row) * H + hcol + 8 * j) = v;
+              *reinterpret_cast<float4*>(Y + (size_t)(rb + row) * H + hcol) = v;
           }
         }
+        if (cc + 1 < NC) __syncthreads();  // the next tile reuses s_y
       }
     });
     __syncthreads();

@@ -7,7 +7,8 @@
 //                    deterministic token-ordered compaction of the local
 //                    (token, expert) pairs into per-expert route lists, one
 //                    wave per 64-token chunk.
-// combine_kernel   : per-token sum of the weighted per-route expert outputs in
+// combine_parts_kernel / combine_rows_kernel :
+//                    per-token sum of the weighted per-route expert outputs in
 //                    ascending expert order, then bf16 RNE (the reference does
 //                    fp32 atomics + bf16_convert_kernel, kernels/moe.cu:682,688-695;
 //                    moe_ref.py:134-136 is the order followed here).
@@ -289,22 +290,46 @@ dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
 // out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ),
 // zeros for a token without local routes.  Tokens with exactly one local
 // route are left alone: GEMM2 wrote their rows (bf16 of 0 + y, the same
-// bits).  Workgroup (t, part) covers 256 float4 columns of token t; the
-// token's route rows are loaded before any is used, so a launch costs one
-// memory latency.
-constexpr int COMBINE_PARTS = H / 4 / 256;  // 7
+// bits).  Two launch shapes with the same sums:
+//  * combine_rows_kernel (large T): one workgroup per token row, thread j
+//    covering float4 columns j + 256p (p < 7, each load instruction reads
+//    4 KB contiguous); the next route's row is loaded while the current one
+//    is summed.  One workgroup per 1/7 of a row, issuing a single round of
+//    loads, ran at ~3 TB/s at T = 8192: its ~57k workgroups each ended after
+//    one memory latency, and the launch rate bounded it.
+//  * combine_parts_kernel (small T): workgroup (t, part) covers 256 float4
+//    columns of token t and loads all of the token's route rows before
+//    using any, so the launch costs one memory latency after the route
+//    list; with few tokens, a row per workgroup would leave most CUs idle.
+constexpr int COMBINE_THREADS = 256, COMBINE_COLS = H / 4 / COMBINE_THREADS;  // 7 float4 per thread
+constexpr int COMBINE_ROWS_MIN_T = 4096;
+static_assert(COMBINE_COLS * COMBINE_THREADS * 4 == H, "combine columns");
 
-__global__ void __launch_bounds__(256)
-combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_route, int T,
-               uint16_t* __restrict__ out) {
-  const int t = blockIdx.x;
-  const int i = blockIdx.y * 256 + threadIdx.x;  // float4 column
-  int r[TOP_K], n = 0;
+// The token's route rows (ascending expert; n of them).
+__device__ __forceinline__ int token_routes(const int32_t* __restrict__ token_route, int t, int (&r)[TOP_K]) {
+  int n = 0;
 #pragma unroll
   for (int k = 0; k < TOP_K; ++k) {
     r[k] = token_route[(size_t)t * TOP_K + k];
     n += r[k] >= 0 ? 1 : 0;  // valid routes come first
   }
+  return n;
+}
+
+__device__ __forceinline__ uint2 bf16x4(const float4& a) {
+  uint2 o;
+  o.x = (uint32_t)bf16_rne(a.x) | ((uint32_t)bf16_rne(a.y) << 16);
+  o.y = (uint32_t)bf16_rne(a.z) | ((uint32_t)bf16_rne(a.w) << 16);
+  return o;
+}
+
+__global__ void __launch_bounds__(COMBINE_THREADS)
+combine_parts_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_route, int T,
+                     uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int i = blockIdx.y * COMBINE_THREADS + threadIdx.x;  // float4 column
+  int r[TOP_K];
+  const int n = token_routes(token_route, t, r);
   if (n == 1) return;
   float4 y[TOP_K];
 #pragma unroll
@@ -314,10 +339,43 @@ combine_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_ro
 #pragma unroll
   for (int k = 0; k < TOP_K; ++k)
     if (k < n) { acc.x += y[k].x; acc.y += y[k].y; acc.z += y[k].z; acc.w += y[k].w; }
-  uint2 o;
-  o.x = (uint32_t)bf16_rne(acc.x) | ((uint32_t)bf16_rne(acc.y) << 16);
-  o.y = (uint32_t)bf16_rne(acc.z) | ((uint32_t)bf16_rne(acc.w) << 16);
-  reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = o;
+  reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = bf16x4(acc);
+}
+
+__global__ void __launch_bounds__(COMBINE_THREADS)
+combine_rows_kernel(const float* __restrict__ Y, const int32_t* __restrict__ token_route, int T,
+                    uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  int r[TOP_K];
+  const int n = token_routes(token_route, t, r);
+  if (n == 1) return;
+  float4 acc[COMBINE_COLS], cur[COMBINE_COLS];
+  auto load = [&](float4 (&y)[COMBINE_COLS], int row) {
+    const float4* src = reinterpret_cast<const float4*>(Y + (size_t)row * H) + tid;
+#pragma unroll
+    for (int p = 0; p < COMBINE_COLS; ++p) y[p] = src[p * COMBINE_THREADS];
+  };
+#pragma unroll
+  for (int p = 0; p < COMBINE_COLS; ++p) acc[p] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n > 0) load(cur, r[0]);
+#pragma unroll
+  for (int k = 0; k < TOP_K; ++k) {
+    if (k >= n) break;
+    float4 nxt[COMBINE_COLS];
+    if (k + 1 < n) load(nxt, r[k + 1 < TOP_K ? k + 1 : k]);
+#pragma unroll
+    for (int p = 0; p < COMBINE_COLS; ++p) {
+      acc[p].x += cur[p].x; acc[p].y += cur[p].y; acc[p].z += cur[p].z; acc[p].w += cur[p].w;
+    }
+    if (k + 1 < n) {
+#pragma unroll
+      for (int p = 0; p < COMBINE_COLS; ++p) cur[p] = nxt[p];
+    }
+  }
+  uint2* dst = reinterpret_cast<uint2*>(out + (size_t)t * H) + tid;
+#pragma unroll
+  for (int p = 0; p < COMBINE_COLS; ++p) dst[p * COMBINE_THREADS] = bf16x4(acc[p]);
 }
 
 hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
@@ -346,7 +404,10 @@ hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, 
 hipError_t launch_combine(const float* Y, const int32_t* token_route, int T, uint16_t* out,
                           hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  combine_kernel<<<dim3(T, COMBINE_PARTS), 256, 0, stream>>>(Y, token_route, T, out);
+  if (T >= COMBINE_ROWS_MIN_T)
+    combine_rows_kernel<<<T, COMBINE_THREADS, 0, stream>>>(Y, token_route, T, out);
+  else
+    combine_parts_kernel<<<dim3(T, COMBINE_COLS), COMBINE_THREADS, 0, stream>>>(Y, token_route, T, out);
   return hipGetLastError();
 }
 
