@@ -209,10 +209,8 @@ __device__ __forceinline__ uint32_t a_lane_offset(int lane) {
 
 // 32x32x64 A operand of K half kh from a K-block base (t0's tile in the
 // slab) plus a_lane_offset.
-// NT: non-temporal loads (the weights stream past the caches).  Taken when
-// each weight block is read by about one route tile (T <= 2048: T=1024 GEMM1
-// 155 -> 135 us); where several route tiles of an expert re-read a weight
-// block from L2 (T=8192, skewed routing) the cached loads stay faster.
+// NT: non-temporal loads (the weights stream past the caches), for items
+// whose weight block no other item reads.
 template <bool NT>
 __device__ __forceinline__ v8i weight_half(const uint8_t* __restrict__ kblock_lane, int kh) {
   if constexpr (NT) {
@@ -324,7 +322,7 @@ __device__ __forceinline__ int d_row(int r, int lane) { return 8 * (r >> 2) + 4 
 // of expert e.  Wave w owns gate tile 2w and up tile 2w+1 of the slab (gate
 // rows nb*128+16w.., up rows 2048+nb*128+16w..) as one 32-row A operand.
 // ---------------------------------------------------------------------------
-template <int CT, int WS, int AS, bool NTW>
+template <int CT, int WS, int AS>
 __global__ void __launch_bounds__(NWAVES * 64)
 stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__ hscale,
                    const uint8_t* __restrict__ w13p, const float* __restrict__ w13s,
@@ -387,14 +385,19 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(2 * w) * TILE_BYTES + alane;
     // One instantiation of the item body per route-tile count (prologue, K
     // loop and epilogue), so no accumulator crosses between them.
-    with_tile_count<CT>(ncc, [&](auto nct) {
+    // The weights of an expert with a single route tile are read by one
+    // item only: those items load them non-temporally (streamed past the
+    // caches); items of an expert with several route tiles, whose tiles
+    // re-read each weight block from L2, load them cached.
+    const bool stream_weights = s_tp[e + 1] - s_tp[e] == 1;
+    auto item = [&](auto ntc, auto nct) __attribute__((always_inline)) {
       constexpr int NC = decltype(nct)::value;
       constexpr int NI = active_chunks<CT>(NC);
       v8i wf[WS][2];
       auto wload = [&](int kb, int sl) {
         const uint8_t* pk = wp + (size_t)kb * W13_KB_BYTES;
-        wf[sl][0] = weight_half<NTW>(pk, 0);
-        wf[sl][1] = weight_half<NTW>(pk, 1);
+        wf[sl][0] = weight_half<decltype(ntc)::value>(pk, 0);
+        wf[sl][1] = weight_half<decltype(ntc)::value>(pk, 1);
       };
       v16f acc[NC];
 #pragma unroll
@@ -494,7 +497,11 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         const uint4 v = *reinterpret_cast<const uint4*>(s_act + row * CQ_LDS_STRIDE + 16 * (tid & 7));
         *reinterpret_cast<uint4*>(Cq + (size_t)(rb + row) * I + nb * BLK + 16 * (tid & 7)) = v;
       }
-    });
+    };
+    if (stream_weights)
+      with_tile_count<CT>(ncc, [&](auto nct) { item(std::true_type{}, nct); });
+    else
+      with_tile_count<CT>(ncc, [&](auto nct) { item(std::false_type{}, nct); });
     __syncthreads();
   }
 }
@@ -506,7 +513,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 // H block hb = 2hp + w/4, 16-row tiles t0 = 2*(w%4), t0 + 1.
 // Y[r, h] = O[r, h] * weight[r].
 // ---------------------------------------------------------------------------
-template <int CT, int WS, int AS, bool NTW>
+template <int CT, int WS, int AS>
 __global__ void __launch_bounds__(NWAVES * 64)
 stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs, const uint8_t* __restrict__ w2p,
                    const float* __restrict__ w2s, const int32_t* __restrict__ counts,
@@ -572,14 +579,19 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const float* ascl = reinterpret_cast<const float*>(s_scl + (lane & 31)) + (w >> 2);
     const int ncc = __builtin_amdgcn_readfirstlane((rows + RT - 1) / RT);
     const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES + alane;
-    with_tile_count<CT>(ncc, [&](auto nct) {
+    // The weights of an expert with a single route tile are read by one
+    // item only: those items load them non-temporally (streamed past the
+    // caches); items of an expert with several route tiles, whose tiles
+    // re-read each weight block from L2, load them cached.
+    const bool stream_weights = s_tp[e + 1] - s_tp[e] == 1;
+    auto item = [&](auto ntc, auto nct) __attribute__((always_inline)) {
       constexpr int NC = decltype(nct)::value;
       constexpr int NI = active_chunks<CT>(NC);
       v8i wf[WS][2];
       auto wload = [&](int kb, int sl) {
         const uint8_t* pk = wp + (size_t)kb * W2_KB_BYTES;
-        wf[sl][0] = weight_half<NTW>(pk, 0);
-        wf[sl][1] = weight_half<NTW>(pk, 1);
+        wf[sl][0] = weight_half<decltype(ntc)::value>(pk, 0);
+        wf[sl][1] = weight_half<decltype(ntc)::value>(pk, 1);
       };
       v16f acc[NC];
 #pragma unroll
@@ -659,7 +671,11 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
         }
         if (cc + 1 < NC) __syncthreads();  // the next tile reuses s_y
       }
-    });
+    };
+    if (stream_weights)
+      with_tile_count<CT>(ncc, [&](auto nct) { item(std::true_type{}, nct); });
+    else
+      with_tile_count<CT>(ncc, [&](auto nct) { item(std::false_type{}, nct); });
     __syncthreads();
   }
 }
@@ -669,27 +685,26 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 // 128-route tiles up to 128 expected routes, 192-route tiles above.  GEMM2
 // always takes 192-route tiles.
 bool stage1_wide_tiles(int T) { return T / 32 > 128; }
-bool nt_weights(int T) { return T <= 2048; }
 
-template <int CT, int WS, int AS, bool NTW>
+template <int CT, int WS, int AS>
 hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
                            const int32_t* counts, const int32_t* offsets, const int32_t* route_token, uint8_t* Cq,
                            float* Cs, int T, int e_local, int max_routes, int32_t* queue, hipStream_t stream) {
   using G = TileGeom<CT>;
-  auto k = stage1_tile_kernel<CT, WS, AS, NTW>;
+  auto k = stage1_tile_kernel<CT, WS, AS>;
   const long long bound = ((long long)e_local + max_routes / G::BM + 1) * IB;
   const int grid = persistent_grid(bound, resident_blocks(k, G::NT));
   k<<<grid, G::NT, 0, stream>>>(hidden, hs, w13p, w13s, counts, offsets, route_token, Cq, Cs, T, e_local, queue);
   return hipGetLastError();
 }
 
-template <int CT, int WS, int AS, bool NTW>
+template <int CT, int WS, int AS>
 hipError_t run_stage2_tile(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2s,
                            const int32_t* counts, const int32_t* offsets, const float* rw,
                            const int32_t* route_token, float* Y, uint16_t* out, int e_local, int max_routes,
                            int32_t* queue, hipStream_t stream) {
   using G = TileGeom<CT>;
-  auto k = stage2_tile_kernel<CT, WS, AS, NTW>;
+  auto k = stage2_tile_kernel<CT, WS, AS>;
   const long long bound = ((long long)e_local + max_routes / G::BM + 1) * (HB / 2);
   const int grid = persistent_grid(bound, resident_blocks(k, G::NT));
   k<<<grid, G::NT, 0, stream>>>(Cq, Cs, w2p, w2s, counts, offsets, rw, route_token, Y, out, e_local, queue);
@@ -702,25 +717,20 @@ hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local, int max_routes,
                          int32_t* queue, hipStream_t stream) {
-  if (nt_weights(T))
-    return run_stage1_tile<4, 2, 2, true>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
-                                          Cs, T, e_local, max_routes, queue, stream);
   if (!stage1_wide_tiles(T))
-    return run_stage1_tile<4, 2, 2, false>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq,
-                                           Cs, T, e_local, max_routes, queue, stream);
-  return run_stage1_tile<6, 2, 1, false>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs,
-                                         T, e_local, max_routes, queue, stream);
+    return run_stage1_tile<4, 2, 2>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
+                                    e_local, max_routes, queue, stream);
+  return run_stage1_tile<6, 2, 1>(hidden, hidden_scale, w13p, w13_scale, counts, offsets, route_token, Cq, Cs, T,
+                                  e_local, max_routes, queue, stream);
 }
 
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
                          const int32_t* route_token, float* Y, uint16_t* out,
-                         int T, int e_local, int max_routes, int32_t* queue, hipStream_t stream) {
-  if (nt_weights(T))
-    return run_stage2_tile<6, 2, 1, true>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, route_token, Y, out,
-                                          e_local, max_routes, queue, stream);
-  return run_stage2_tile<6, 2, 1, false>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, route_token, Y, out,
-                                         e_local, max_routes, queue, stream);
+                         int /*T: one tile shape for every T*/, int e_local, int max_routes, int32_t* queue,
+                         hipStream_t stream) {
+  return run_stage2_tile<6, 2, 1>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, route_token, Y, out, e_local,
+                                  max_routes, queue, stream);
 }
 
 }  // namespace moe
