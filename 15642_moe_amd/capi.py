@@ -63,6 +63,7 @@ SIGNATURES = {
     "moe_router_quant": (_c_int, [_c_vp, _c_vp, _c_int, _c_vp, _c_size, _c_vp, _c_vp, _c_vp, _c_vp]),
     "moe_fill_normal_e4m3": (_c_int, [_c_vp, _c_size, _c_u64, _c_u64, _c_vp]),
     "moe_mfma_tiles": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_vp]),
+    "moe_mfma_ceiling": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp]),
     "moe_host_fill_normal_e4m3": (_c_int, [_c_vp, _c_size, _c_u64, _c_u64, _c_u64, _c_int]),
 }
 

@@ -388,6 +388,16 @@ int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream) 
                     "mfma_tile_kernel launch");
 }
 
+int moe_mfma_ceiling(float* out, uint64_t* clocks, int iters, int grid, void* stream) {
+  if (iters < 1 || iters > (1 << 20)) return fail(MOE_ERR_INVALID_ARG, "iters must be in [1, 2^20], got %d", iters);
+  if (grid < 1 || grid > 65536) return fail(MOE_ERR_INVALID_ARG, "grid must be in [1, 65536], got %d", grid);
+  MOE_TRY(check_ptr(out, "out"));
+  MOE_TRY(check_ptr(clocks, "clocks"));
+  return hip_status(moe::launch_mfma_ceiling(out, reinterpret_cast<unsigned long long*>(clocks), iters, grid,
+                                             reinterpret_cast<hipStream_t>(stream)),
+                    "mfma_ceiling_kernel launch");
+}
+
 int moe_host_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id, uint64_t first_index,
                               int threads) {
   if (n == 0) return MOE_OK;

@@ -367,6 +367,49 @@ hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n
   return hipGetLastError();
 }
 
+// FP8 MFMA throughput with nothing else in the loop: each of a workgroup's
+// 8 waves (2 per SIMD, as in the prefill GEMMs) chains `iters` rounds of 4
+// independent 32x32x64 MFMAs on register operands (fixed finite e4m3 bit
+// patterns: bit 3 of each byte clear keeps the exponent field below 15).
+// Thread 0 stores the workgroup's elapsed constant-rate (100 MHz) and
+// shader-clock counter ticks, whose ratio is the mean shader clock.
+__global__ void __launch_bounds__(MFMA_CEILING_THREADS) mfma_ceiling_kernel(float* __restrict__ out,
+                                                           unsigned long long* __restrict__ clocks, int iters) {
+  const int lane = threadIdx.x & 63;
+  v8i a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = (int)((0x3C5A1E97u * (unsigned)(lane + 1) + 0x9E3779B9u * (unsigned)i) & 0xF7F7F7F7u);
+    b[i] = (int)((0x2B7E1516u * (unsigned)(lane + 3) + 0x7F4A7C15u * (unsigned)i) & 0xF7F7F7F7u);
+  }
+  v16f acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime(), c0 = __builtin_amdgcn_s_memtime();
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = mfma_32x32x64_fp8(a, b, acc[j]);
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime(), c1 = __builtin_amdgcn_s_memtime();
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[j][r];
+  out[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+  if (threadIdx.x == 0) {
+    clocks[2 * (size_t)blockIdx.x] = t1 - t0;
+    clocks[2 * (size_t)blockIdx.x + 1] = c1 - c0;
+  }
+}
+
+hipError_t launch_mfma_ceiling(float* out, unsigned long long* clocks, int iters, int grid, hipStream_t stream) {
+  mfma_ceiling_kernel<<<grid, MFMA_CEILING_THREADS, 0, stream>>>(out, clocks, iters);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers.
 // ---------------------------------------------------------------------------

@@ -57,5 +57,10 @@ hipError_t launch_router_quant(const uint8_t* hidden_bf16, const uint8_t* router
                                float* logits, uint8_t* hidden_fp8, float* hidden_scale, hipStream_t stream);
 
 hipError_t launch_mfma_tiles(const uint8_t* A, const uint8_t* B, float* D, int n, hipStream_t stream);
+// FP8 MFMA loop of `grid` workgroups of MFMA_CEILING_THREADS threads: out
+// [grid * MFMA_CEILING_THREADS] fp32, clocks [grid][2] (100 MHz ticks, shader
+// clock ticks).
+constexpr int MFMA_CEILING_THREADS = 512;
+hipError_t launch_mfma_ceiling(float* out, unsigned long long* clocks, int iters, int grid, hipStream_t stream);
 
 }  // namespace moe

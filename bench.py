@@ -233,9 +233,12 @@ def main() -> int:
         del inp, p13, p2, args_fwd, out, ws, evs, kw
         torch.cuda.empty_cache()
 
+    ceiling = _mfma_ceiling(torch, lib, dev, capi)
+    for rec in results.values():
+        rec["stage_frac_of_mfma_ceiling"] = {k: round(v / ceiling["tflops"], 4) for k, v in rec["stage_tflops"].items()}
     if args.no_headline:
-        print(json.dumps({"metric": METRIC, "configs": results, "cpu_baseline_per_config": cpu_runs or None}),
-              flush=True)
+        print(json.dumps({"metric": METRIC, "configs": results, "mfma_ceiling": ceiling,
+                          "cpu_baseline_per_config": cpu_runs or None}), flush=True)
         return 0
     upstream = [] if args.no_upstream else [
         _time_upstream(torch, lib, dev, inputs_mod.CONFIGS[i].T, args.steps) for i in cfg_ids]
@@ -296,10 +299,50 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "configs": results,
+        "mfma_ceiling": ceiling,
         "upstream": upstream,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _mfma_ceiling(torch, lib, dev, capi) -> dict:
+    """The FP8 MFMA rate this GPU sustains with nothing but MFMAs in flight
+    (moe_mfma_ceiling: one 512-thread workgroup per CU, 4 independent
+    32x32x64 MFMA chains per wave, ~2 ms per launch), and the mean shader
+    clock it ran at.  Dense FP8 work on every CU draws enough power that the
+    clock drops well below its maximum, so this, not the published peak, is
+    the rate a compute-bound kernel can approach; the prefill GEMMs'
+    stage_frac_of_mfma_ceiling compares them with it.  Median of 5 timed
+    launches after one warm-up launch."""
+    grid = torch.cuda.get_device_properties(dev).multi_processor_count
+    iters = 4000
+    flops = grid * 8 * iters * 4 * 2 * 32 * 32 * 64
+    out = torch.empty(grid * 512, dtype=torch.float32, device=dev)
+    clocks = torch.zeros(grid * 2, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    rates, mhz = [], []
+    for rep in range(6):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        capi.check(lib.moe_mfma_ceiling(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(clocks.data_ptr()), iters,
+                                        grid, ctypes.c_void_p(stream.cuda_stream)), "moe_mfma_ceiling")
+        end.record(stream)
+        torch.cuda.synchronize()
+        if rep == 0:
+            continue
+        c = clocks.view(grid, 2).cpu().double()
+        rates.append(flops / (start.elapsed_time(end) * 1e-3) / 1e12)
+        mhz.append(100.0 * c[:, 1].sum().item() / c[:, 0].sum().item())
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError("moe_mfma_ceiling produced non-finite sums")
+    rates.sort()
+    mhz.sort()
+    rec = {"kernel": "mfma_ceiling_kernel (fp8 32x32x64, register operands, no memory traffic)",
+           "tflops": round(rates[len(rates) // 2], 1), "clock_mhz": round(mhz[len(mhz) // 2]),
+           "frac_of_peak": round(rates[len(rates) // 2] / FP8_PEAK_TFLOPS, 4), "workgroups": grid, "iters": iters}
+    log(f"mfma ceiling: {json.dumps(rec)}")
+    return rec
 
 
 def _cpu_baseline(inputs_cpu: dict, cfg, gpu_us: float, budget_s: float) -> dict:

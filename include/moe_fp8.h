@@ -197,6 +197,19 @@ int moe_host_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t strea
  */
 int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream);
 
+/*
+ * Measurement instrumentation, no counterpart in the reference: the FP8
+ * MFMA rate the chip sustains with nothing but MFMAs in flight.  `grid`
+ * workgroups of 512 threads each run `iters` rounds of 4 independent
+ * 32x32x64 FP8 MFMAs per wave on register operands (2 waves per SIMD, as
+ * in the prefill GEMMs); 2 * 32 * 32 * 64 * 4 * 8 * iters FLOPs per
+ * workgroup.  out: [grid * 512] fp32 (the accumulator sums, finite);
+ * clocks: [grid][2] uint64 per workgroup, elapsed ticks of the constant
+ * 100 MHz counter and of the shader clock (their ratio x 100 MHz is the
+ * mean shader clock while it ran).  iters in [1, 2^20], grid in [1, 65536].
+ */
+int moe_mfma_ceiling(float* out, uint64_t* clocks, int iters, int grid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

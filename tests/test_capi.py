@@ -117,6 +117,9 @@ def test_route_and_pack_validation(lib, capi):
     assert lib.moe_pack_w2(FAKE, FAKE, 0, None) == capi.MOE_ERR_INVALID_ARG
     assert lib.moe_unpack_w2(FAKE, ctypes.c_void_p(0x10001), 1, None) == capi.MOE_ERR_INVALID_ARG
     assert lib.moe_fill_normal_e4m3(None, 16, 1, 1, None) == capi.MOE_ERR_INVALID_ARG
+    assert lib.moe_mfma_ceiling(FAKE, FAKE, 0, 8, None) == capi.MOE_ERR_INVALID_ARG
+    assert lib.moe_mfma_ceiling(FAKE, FAKE, 16, 0, None) == capi.MOE_ERR_INVALID_ARG
+    assert lib.moe_mfma_ceiling(None, FAKE, 16, 8, None) == capi.MOE_ERR_INVALID_ARG
 
 
 def test_capi_check_raises_runtime_error(lib, capi):

@@ -54,6 +54,25 @@ def test_mfma_block_sum_accuracy(capi, lib, cuda, dist):
     assert rel.max() <= MFMA_REL_BOUND
 
 
+def test_mfma_ceiling_probe(capi, lib, cuda):
+    """The bench's MFMA-rate probe: finite sums, and per-workgroup counter
+    ticks whose ratio is a plausible shader clock."""
+    import ctypes
+
+    grid, iters = 16, 64
+    out = torch.full((grid * 512,), float("nan"), dtype=torch.float32, device=cuda)
+    clocks = torch.zeros(grid * 2, dtype=torch.int64, device=cuda)
+    capi.check(lib.moe_mfma_ceiling(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(clocks.data_ptr()), iters,
+                                    grid, None), "moe_mfma_ceiling")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    c = clocks.view(grid, 2).cpu()
+    assert bool((c > 0).all())
+    mhz = 100.0 * c[:, 1].sum().item() / c[:, 0].sum().item()
+    print(f"[mfma ceiling probe] mean shader clock {mhz:.0f} MHz", flush=True)
+    assert 300.0 < mhz < 4000.0
+
+
 def test_pack_matches_oracle_permutation(ops, cuda):
     g = torch.Generator(device="cpu").manual_seed(5)
     w13 = torch.randint(0, 256, (2, 4096, 7168), dtype=torch.uint8, generator=g)
