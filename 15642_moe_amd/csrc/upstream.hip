@@ -255,13 +255,17 @@ logits_reduce_kernel(const float4* __restrict__ part, int n_kp, int n4, float4* 
 
 }  // namespace
 
-// K parts per launch: enough workgroups to cover the CUs, each part a
-// multiple of the ring depth in K-blocks.
+// K parts per launch: the fewest that give at least 448 workgroups (about
+// two per CU; the K loop's dependent steps leave one workgroup per CU short
+// of the HBM rate), each part a multiple of the ring depth in K-blocks.
+// Measured: T=4096 51.5 -> 42.7 us with 2 parts (512 workgroups) instead of
+// 1; more parts than that lose to the partial sums' traffic and reduction
+// (T=8192 with 2 parts: 77 -> 81 us; T=1024 with 14: 19.9 -> 25.5 us).
 int router_k_parts(int T) {
   const int groups = RQ_EQ * ((T + RQ_TOK - 1) / RQ_TOK);
   const int parts[] = {1, 2, 7, 14};
   for (int p : parts)
-    if (groups * p >= 256) return p;
+    if (groups * p >= 448) return p;
   return 14;
 }
 
