@@ -74,7 +74,7 @@ __device__ __forceinline__ float row16_max(float m) {
 }
 
 // The K loop's memory operations are inline assembly in a fixed order (per
-// K-block: the 8 loads of the block three ahead, then the code store)
+// K-block: the code store, then the 8 loads of the block three ahead)
 // waited for with explicit counts: the compiler's own waits, merged
 // at the loop head across the unrolled ring and the loop's stores, drained
 // every load there.  The registers of a block pass through an empty asm
@@ -157,16 +157,35 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
   };
 #pragma unroll
   for (int sl = 0; sl < RQ_NR - 1; ++sl) load(kb0 + sl, sl);
-  // One K-block: issue the loads three blocks ahead, wait for this block's
-  // loads, quantise, stage, multiply.  Block kb's loads are older than
-  // exactly WAIT operations: 27 in steady state (its code store, two
-  // K-blocks of 8 loads + 1 store, the 8 loads just issued), 24 / 25 / 26 in
-  // the first three blocks (the prologue loads have no stores between them).
+  // The MFMAs of a K-block run one step late, between the next block's
+  // staging stores and the step's barrier: they read the other LDS buffer
+  // (staged a step earlier, behind the previous barrier), so neither the
+  // LDS reads nor the MFMAs wait on this step's barrier, and the barrier's
+  // wait for the slowest wave's stores overlaps them.  Buffer (kb - kb0) & 1
+  // is restaged only after every wave passed the barrier that follows its
+  // MFMAs.  The loads three blocks ahead are issued after those MFMAs,
+  // into the ring slot whose weights they have just used.
+  auto mma = [&](const uint8_t* sb, const u32x4 (&aw)[RQ_KS]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < RQ_KS; ++ks) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const v8bf b = *reinterpret_cast<const v8bf*>(sb + rslot[ks] + tt * RQ_KS * RQ_FRAG);
+        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, aw[ks]), b, acc[tt], 0, 0, 0);
+      }
+    }
+  };
+  // One K-block: wait for its loads, quantise, stage, multiply the previous
+  // block, issue the loads three blocks ahead.  Block kb's loads are older
+  // than exactly WAIT operations: 18 in steady state (two K-blocks of code
+  // store + 8 loads), 16 / 17 in the first two blocks (the prologue loads
+  // have no stores between them).
   int kq = 0;
-  auto step = [&](auto sl_c, auto wait_c) {
+  auto step = [&](auto sl_c, auto wait_c, auto prev_c) {
     constexpr int sl = decltype(sl_c)::value, WAIT = decltype(wait_c)::value;
+    constexpr bool PREV = decltype(prev_c)::value;  // a previous block to multiply
+    constexpr int ps = (sl + RQ_NR - 1) % RQ_NR;       // its ring slot, refilled after its MFMAs
     const int kb = kb0 + kq + sl;
-    load(min(kb + RQ_NR - 1, kb0 + kpb - 1), (sl + RQ_NR - 1) % RQ_NR);  // branch-free; the tail re-reads
     wait_vm<WAIT>();
 #pragma unroll
     for (int i = 0; i < 4; ++i) __asm__ volatile("" : "+v"(v[sl][i]));
@@ -194,34 +213,30 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
       gstore2(qoff, codes, hq + (size_t)kb * BLK);
       if ((tid & 15) == 0) s_qs[kb - kb0][tid >> 4] = sc;
     }
-    // Stage the block as B fragments; buffer (kb - kb0) & 1 was last read
-    // two blocks ago, before every wave passed the previous barrier.
     uint8_t* sb = s_b[sl & 1];
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4*>(sb + sslot[i]) = v[sl][i];
+    if constexpr (PREV) mma(s_b[(sl + 1) & 1], a[ps]);
+    load(min(kb + RQ_NR - 1, kb0 + kpb - 1), ps);  // branch-free; the tail re-reads
     __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < RQ_KS; ++ks) {
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const v8bf b = *reinterpret_cast<const v8bf*>(sb + rslot[ks] + tt * RQ_KS * RQ_FRAG);
-        acc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a[sl][ks]), b, acc[tt], 0, 0, 0);
-      }
-    }
   };
   using std::integral_constant;
-  step(integral_constant<int, 0>{}, integral_constant<int, 24>{});
-  step(integral_constant<int, 1>{}, integral_constant<int, 25>{});
-  step(integral_constant<int, 2>{}, integral_constant<int, 26>{});
-  step(integral_constant<int, 3>{}, integral_constant<int, 27>{});
+  using std::true_type;
+  step(integral_constant<int, 0>{}, integral_constant<int, 16>{}, std::false_type{});
+  step(integral_constant<int, 1>{}, integral_constant<int, 17>{}, true_type{});
+  step(integral_constant<int, 2>{}, integral_constant<int, 18>{}, true_type{});
+  step(integral_constant<int, 3>{}, integral_constant<int, 18>{}, true_type{});
 #pragma unroll 1
   for (kq = RQ_NR; kq < kpb; kq += RQ_NR) {
-    step(integral_constant<int, 0>{}, integral_constant<int, 27>{});
-    step(integral_constant<int, 1>{}, integral_constant<int, 27>{});
-    step(integral_constant<int, 2>{}, integral_constant<int, 27>{});
-    step(integral_constant<int, 3>{}, integral_constant<int, 27>{});
+    step(integral_constant<int, 0>{}, integral_constant<int, 18>{}, true_type{});
+    step(integral_constant<int, 1>{}, integral_constant<int, 18>{}, true_type{});
+    step(integral_constant<int, 2>{}, integral_constant<int, 18>{}, true_type{});
+    step(integral_constant<int, 3>{}, integral_constant<int, 18>{}, true_type{});
   }
   wait_vm<0>();  // the dead tail loads land before the registers are reused
+  // the last block (ring slot 3, LDS buffer 1: kpb is a multiple of 4),
+  // staged before the last step's barrier
+  mma(s_b[1], a[RQ_NR - 1]);
   __syncthreads();
   // Scales of the 16 quantised rows, [kb][T] layout: 16 consecutive tokens per K-block.
   for (int j = tid; j < kpb * 16; j += RQ_NT) {
