@@ -189,7 +189,7 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    wait_vm<0>();  // the dead tail loads land before the registers are reused
+    wait_vm_all();  // the dead tail loads land before the registers are reused
 #pragma unroll
     for (int f = 0; f < FR; ++f) {
       if (col < rows[f]) {
@@ -318,7 +318,7 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    wait_vm<0>();
+    wait_vm_all();
 #pragma unroll
     for (int f = 0; f < FR; ++f) {
       if (col < rows[f]) {

@@ -48,6 +48,14 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
+// A ring's final wait, after which the dead tail loads' registers may be
+// reused: the compiler sees those registers as free once their (unused)
+// asm outputs are defined, and the scheduling barrier keeps every later
+// instruction -- whose temporaries may land in them -- below the wait.
+__device__ __forceinline__ void wait_vm_all() {
+  wait_vm<0>();
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 // 32-byte operand fragment of one 2 KB tile in split-half layout:
 // half h of lane l at h*1024 + l*16 (global or LDS).

@@ -93,6 +93,13 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
   __asm__ volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
+// The ring's final wait; the scheduling barrier keeps every later
+// instruction, whose temporaries may take the dead tail loads' registers,
+// below it.
+__device__ __forceinline__ void wait_vm_all() {
+  wait_vm<0>();
+  __builtin_amdgcn_sched_barrier(0);
+}
 
 // LDS slot of the B fragment (token tile tt, K step ks) for token i, chunk
 // g: fragment lane 16g + i, stored at position 16g + (i ^ (c & 7)) with
@@ -233,7 +240,7 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
     step(integral_constant<int, 2>{}, integral_constant<int, 18>{}, true_type{});
     step(integral_constant<int, 3>{}, integral_constant<int, 18>{}, true_type{});
   }
-  wait_vm<0>();  // the dead tail loads land before the registers are reused
+  wait_vm_all();  // the dead tail loads land before the registers are reused
   // the last block (ring slot 3, LDS buffer 1: kpb is a multiple of 4),
   // staged before the last step's barrier
   mma(s_b[1], a[RQ_NR - 1]);
