@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in include/moe_fp8.h.
+"""ctypes binding of the C ABI in include/moe_fp8.h (and the test and
+measurement instrumentation of include/moe_fp8_testing.h, same library).
 
 The shared library is built in-tree by ``build.py``.  Loading it never falls
 back to anything: a missing or stale library raises RuntimeError.  torch is
@@ -28,7 +29,8 @@ FORWARD_EVENTS = 6
 
 _c_int, _c_size, _c_float, _c_vp, _c_u64 = ctypes.c_int, ctypes.c_size_t, ctypes.c_float, ctypes.c_void_p, ctypes.c_uint64
 
-# name -> (restype, argtypes); exactly the functions include/moe_fp8.h declares.
+# name -> (restype, argtypes); exactly the functions include/moe_fp8.h and
+# include/moe_fp8_testing.h declare.
 SIGNATURES = {
     "moe_abi_version": (_c_int, []),
     "moe_last_error": (ctypes.c_char_p, []),

@@ -3,6 +3,7 @@
 #include "common.h"
 #include "launch.h"
 #include "moe_fp8.h"
+#include "moe_fp8_testing.h"
 
 #include <cstdarg>
 #include <cstdio>

@@ -238,7 +238,12 @@ def moe_forward(hidden, hidden_scale, W13_packed, W13_scale, W2_packed, W2_scale
 
 # --------------------------------------------------------------------------- inspection
 def workspace_views(ws: torch.Tensor, T: int, E: int) -> dict:
-    """Typed views of the MOE_WS_* buffers inside a forward/route workspace."""
+    """Typed views of the MOE_WS_* buffers inside a forward/route workspace.
+
+    ``Y`` rows of routes whose ``route_token`` entry has bit 31 set (the
+    token's only local route) are not written by the forward: GEMM2 writes
+    that token's bf16 output row directly, so those Y rows hold stale data.
+    """
     off = capi.workspace_offsets(T, E)
     R = T * min(TOP_K, E)
 

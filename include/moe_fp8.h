@@ -50,7 +50,10 @@ enum moe_ws_buffer {
   MOE_WS_TOKEN_ROUTE,   /* int32 [T, 8]  routes of each token, ascending, -1   */
   MOE_WS_CQ,            /* e4m3  [R, I]  SwiGLU output, block-quantised        */
   MOE_WS_CS,            /* f32   [R, 16] its per-128-block scales              */
-  MOE_WS_Y,             /* f32   [R, H]  weighted expert outputs per route     */
+  MOE_WS_Y,             /* f32   [R, H]  weighted expert outputs per route;
+                           rows of routes whose MOE_WS_ROUTE_TOKEN entry has
+                           bit 31 set are NOT written (the token's only local
+                           route: its value goes straight to out_bf16)       */
   MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/64)]  work-queue counters of the
                            prefill GEMMs (zeroed by the dispatch of every
                            forward), then the dispatch's per-chunk counts      */
@@ -172,43 +175,6 @@ int moe_unpack_router(const void* router_packed, void* router_w_bf16, void* stre
 size_t moe_router_workspace_bytes(int T);
 int moe_router_quant(const void* hidden_bf16, const void* router_packed, int T, void* workspace,
                      size_t workspace_bytes, float* logits, void* hidden_fp8, float* hidden_scale, void* stream);
-
-/*
- * Synthetic e4m3 data, ~N(0,1) (Irwin-Hall of four 16-bit hash fields),
- * bit-identical to the host generator for the same (seed, stream_id).
- * Test/benchmark input synthesis; no counterpart in the reference.
- */
-int moe_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id, void* stream);
-
-/*
- * Host (CPU) twin of moe_fill_normal_e4m3 writing elements
- * [first_index, first_index + n) of the same sequence into host memory, on
- * `threads` CPU threads (<= 0: all).  Needs no GPU.
- */
-int moe_host_fill_normal_e4m3(void* out, size_t n, uint64_t seed, uint64_t stream_id, uint64_t first_index,
-                              int threads);
-
-/*
- * n independent 16x16 products D[t] = A[t] (16x128 e4m3, row-major) x B[t]
- * (128x16 e4m3, given as 16 columns of 128 contiguous K bytes) through the
- * FP8 MFMA instruction the GEMMs use; D fp32 [n, 16, 16] row-major.  Test
- * instrumentation for the instruction's accumulation accuracy; no
- * counterpart in the reference.
- */
-int moe_mfma_tiles(const void* a, const void* b, float* d, int n, void* stream);
-
-/*
- * Measurement instrumentation, no counterpart in the reference: the FP8
- * MFMA rate the chip sustains with nothing but MFMAs in flight.  `grid`
- * workgroups of 512 threads each run `iters` rounds of 4 independent
- * 32x32x64 FP8 MFMAs per wave on register operands (2 waves per SIMD, as
- * in the prefill GEMMs); 2 * 32 * 32 * 64 * 4 * 8 * iters FLOPs per
- * workgroup.  out: [grid * 512] fp32 (the accumulator sums, finite);
- * clocks: [grid][2] uint64 per workgroup, elapsed ticks of the constant
- * 100 MHz counter and of the shader clock (their ratio x 100 MHz is the
- * mean shader clock while it ran).  iters in [1, 2^20], grid in [1, 65536].
- */
-int moe_mfma_ceiling(float* out, uint64_t* clocks, int iters, int grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,4 +1,6 @@
-"""C ABI: the library loads, exports exactly what include/moe_fp8.h declares,
+"""C ABI: the library loads, exports exactly what include/moe_fp8.h (the
+product entry points) and include/moe_fp8_testing.h (test and measurement
+instrumentation) declare,
 and rejects bad arguments before touching the GPU (no compute calls here)."""
 
 from __future__ import annotations
@@ -12,11 +14,22 @@ import pytest
 from conftest import REPO
 
 HEADER = REPO / "include" / "moe_fp8.h"
+TESTING_HEADER = REPO / "include" / "moe_fp8_testing.h"
+INSTRUMENTATION = {"moe_fill_normal_e4m3", "moe_host_fill_normal_e4m3", "moe_mfma_tiles", "moe_mfma_ceiling"}
+
+
+def _declared(path) -> set[str]:
+    text = re.sub(r"/\*.*?\*/", "", path.read_text(), flags=re.S)
+    return set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(moe_\w+)\s*\(", text, flags=re.M))
 
 
 def declared_functions() -> set[str]:
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(moe_\w+)\s*\(", text, flags=re.M))
+    return _declared(HEADER) | _declared(TESTING_HEADER)
+
+
+def test_instrumentation_lives_in_the_testing_header():
+    assert _declared(TESTING_HEADER) == INSTRUMENTATION
+    assert not (_declared(HEADER) & INSTRUMENTATION)
 
 
 def test_header_declares_entry_points():
@@ -27,8 +40,8 @@ def test_header_declares_entry_points():
 def test_library_exports_every_declared_symbol(lib, capi):
     names = declared_functions()
     for name in sorted(names):
-        assert hasattr(lib, name), f"{name} declared in moe_fp8.h but not exported"
-    assert names == set(capi.SIGNATURES), "ctypes prototypes must cover exactly the header"
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    assert names == set(capi.SIGNATURES), "ctypes prototypes must cover exactly the headers"
 
 
 def test_abi_version(lib, capi):
