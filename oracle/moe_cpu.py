@@ -152,30 +152,52 @@ def forward_full_dequant(inputs: dict) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------------- kernel semantics
-def _fma32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+def _fma32(a, b, c):
     """fp32 fused multiply-add (exact product and sum in float64, one final
-    rounding; double rounding through float64 is ignored)."""
-    return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
+    rounding; double rounding through float64 is ignored).  Accepts numpy
+    arrays or torch tensors (torch runs the elementwise work on all host
+    threads); returns the same kind as `a`."""
+    if isinstance(a, np.ndarray):
+        return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
+    return (a.double() * b.double() + c.double()).float()
 
 
-def _block_sums(a: np.ndarray, w: np.ndarray, nblk: int) -> np.ndarray:
-    """Exact per-128-K block dot products rounded to fp32.
-    a: [R, nblk*128] bytes, w: [N, nblk*128] bytes -> [nblk, R, N]."""
+def weight_operand(w: np.ndarray, nblk: int) -> torch.Tensor:
+    """e4m3 weight bytes [N, nblk*128] -> float64 [nblk, 128, N] (the right
+    operand of _block_sums; prepare once per expert and reuse)."""
+    return torch.from_numpy(E4M3_TABLE[w].reshape(w.shape[0], nblk, BLOCK)).permute(1, 2, 0).contiguous()
+
+
+def _block_sums(a: np.ndarray, w: np.ndarray, nblk: int, w_op: torch.Tensor | None = None) -> torch.Tensor:
+    """Exact per-128-K block dot products rounded to fp32 (float64 sums of
+    e4m3 x e4m3 products are exact: each product has 8 significant bits
+    within 2^-18 .. 2^18, so 128 of them fit the 53-bit significand).
+    a: [R, nblk*128] bytes, w: [N, nblk*128] bytes (or w_op, its
+    weight_operand) -> [nblk, R, N] fp32."""
     A = torch.from_numpy(E4M3_TABLE[a].reshape(a.shape[0], nblk, BLOCK)).permute(1, 0, 2)
-    W = torch.from_numpy(E4M3_TABLE[w].reshape(w.shape[0], nblk, BLOCK)).permute(1, 2, 0)
-    return torch.bmm(A, W).to(torch.float32).numpy()
+    W = weight_operand(w, nblk) if w_op is None else w_op
+    return torch.bmm(A, W).to(torch.float32)
 
 
-def stage1_model(a_bytes, a_scale, w13_bytes, w13_scale):
+def _scaled_accumulate(raw: torch.Tensor, a_scale: np.ndarray, w_scale_rows: np.ndarray) -> np.ndarray:
+    """acc = fma(raw[kb], a_scale[:, kb] * w_scale_rows[:, kb], acc) over the
+    K-blocks in order, in fp32 (kernels/moe.cu:468-493, 652-667)."""
+    a_s = torch.from_numpy(np.ascontiguousarray(a_scale, dtype=np.float32))
+    w_s = torch.from_numpy(np.ascontiguousarray(w_scale_rows, dtype=np.float32))
+    acc = torch.zeros(raw.shape[1:], dtype=torch.float32)
+    for kb in range(raw.shape[0]):
+        sc = a_s[:, kb][:, None] * w_s[:, kb][None, :]  # fp32 product, as the kernel forms it
+        acc = _fma32(raw[kb], sc, acc)
+    return acc.numpy()
+
+
+def stage1_model(a_bytes, a_scale, w13_bytes, w13_scale, w_op=None):
     """One expert.  a_bytes [R,7168] u8, a_scale [R,56] f32, w13_bytes
     [4096,7168] u8, w13_scale [32,56] f32 -> (Cq [R,2048] u8, Cs [R,16] f32,
     c [R,2048] f32 before requant)."""
-    raw = _block_sums(a_bytes, w13_bytes, H // BLOCK)                  # [56, R, 4096]
+    raw = _block_sums(a_bytes, w13_bytes, H // BLOCK, w_op)            # [56, R, 4096]
     wsc = np.repeat(np.asarray(w13_scale, np.float32), BLOCK, axis=0)  # [4096, 56]
-    acc = np.zeros(raw.shape[1:], dtype=np.float32)
-    for kb in range(raw.shape[0]):
-        sc = (a_scale[:, kb][:, None] * wsc[:, kb][None, :]).astype(np.float32)
-        acc = _fma32(raw[kb], sc, acc)
+    acc = _scaled_accumulate(raw, a_scale, wsc)
     gate = torch.from_numpy(acc[:, :I])
     up = torch.from_numpy(acc[:, I:])
     c = ((up / (1.0 + torch.exp(-up))) * gate).numpy()
@@ -187,21 +209,24 @@ def stage1_model(a_bytes, a_scale, w13_bytes, w13_scale):
     return e4m3_encode(q.reshape(R, I)), scale, c
 
 
-def stage2_model(cq, cs, w2_bytes, w2_scale):
+def stage2_model(cq, cs, w2_bytes, w2_scale, w_op=None):
     """One expert.  cq [R,2048] u8, cs [R,16] f32, w2_bytes [7168,2048] u8,
     w2_scale [56,16] f32 -> O [R,7168] f32."""
-    raw = _block_sums(cq, w2_bytes, I // BLOCK)                        # [16, R, 7168]
+    raw = _block_sums(cq, w2_bytes, I // BLOCK, w_op)                  # [16, R, 7168]
     wsc = np.repeat(np.asarray(w2_scale, np.float32), BLOCK, axis=0)   # [7168, 16]
-    acc = np.zeros(raw.shape[1:], dtype=np.float32)
-    for ib in range(raw.shape[0]):
-        sc = (cs[:, ib][:, None] * wsc[:, ib][None, :]).astype(np.float32)
-        acc = _fma32(raw[ib], sc, acc)
-    return acc
+    return _scaled_accumulate(raw, cs, wsc)
 
 
-def kernel_model(inputs: dict, ids=None, weights=None, token_subset=None, keep_intermediates: bool = False):
+def kernel_model(inputs: dict, ids=None, weights=None, token_subset=None, keep_intermediates: bool = False,
+                 route_chunk: int = 512, progress=None):
     """FP8-kernel semantics -> dict(out_bf16_bits [T,H] uint16, and per-expert
-    intermediates keyed by local expert when `keep_intermediates`)."""
+    intermediates keyed by local expert when `keep_intermediates`).
+
+    Each expert's routes are modelled `route_chunk` at a time (every route is
+    independent through both GEMMs), which bounds host memory at any T; the
+    per-token sums run in ascending local-expert order, fp32, starting from
+    0 + y (the kernel's combine order).  `progress(local_expert, n_routes)`,
+    when given, is called after each expert."""
     if ids is None:
         r = oracle_routing.route(_f32(inputs["routing_logits"]), _f32(inputs["routing_bias"]),
                                  float(inputs["routed_scaling_factor"]))
@@ -214,29 +239,31 @@ def kernel_model(inputs: dict, ids=None, weights=None, token_subset=None, keep_i
     a_scale = _f32(inputs["hidden_states_scale"])
     s13 = _f32(inputs["gemm1_weights_scale"])
     s2 = _f32(inputs["gemm2_weights_scale"])
-    contrib = {}  # token -> list of (expert, y row)
+    out = np.zeros((T, H), dtype=np.float32)
     inter = {}
     for le in range(E):
         ge = offset + le
         hit = (ids[tokens] == ge).any(axis=1)
         if not hit.any():
             continue
-        tok = tokens[hit]
-        cq, cs, c = stage1_model(a_bytes[tok], a_scale[:, tok].T.copy(), _u8(inputs["gemm1_weights"][le]), s13[le])
-        O = stage2_model(cq, cs, _u8(inputs["gemm2_weights"][le]), s2[le])
-        k = np.argmax(ids[tok] == ge, axis=1)
-        wt = np.asarray(weights)[tok, k].astype(np.float32)
-        Y = (O * wt[:, None]).astype(np.float32)
-        for j, t in enumerate(tok):
-            contrib.setdefault(int(t), []).append((le, Y[j]))
+        tok_all = tokens[hit]
+        w13b, w2b = _u8(inputs["gemm1_weights"][le]), _u8(inputs["gemm2_weights"][le])
+        w13_op, w2_op = weight_operand(w13b, H // BLOCK), weight_operand(w2b, I // BLOCK)
+        parts = []
+        for c0 in range(0, len(tok_all), route_chunk):
+            tok = tok_all[c0:c0 + route_chunk]
+            cq, cs, c = stage1_model(a_bytes[tok], a_scale[:, tok].T.copy(), w13b, s13[le], w13_op)
+            O = stage2_model(cq, cs, w2b, s2[le], w2_op)
+            k = np.argmax(ids[tok] == ge, axis=1)
+            wt = np.asarray(weights)[tok, k].astype(np.float32)
+            Y = (O * wt[:, None]).astype(np.float32)
+            out[tok] = (out[tok] + Y).astype(np.float32)  # a token appears once per expert
+            if keep_intermediates:
+                parts.append(dict(tokens=tok, Cq=cq, Cs=cs, c=c, O=O, Y=Y))
         if keep_intermediates:
-            inter[le] = dict(tokens=tok, Cq=cq, Cs=cs, c=c, O=O, Y=Y)
-    out = np.zeros((T, H), dtype=np.float32)
-    for t, lst in contrib.items():
-        acc = np.zeros(H, dtype=np.float32)
-        for _, y in sorted(lst, key=lambda p: p[0]):
-            acc = (acc + y).astype(np.float32)
-        out[t] = acc
+            inter[le] = {key: np.concatenate([pt[key] for pt in parts]) for key in parts[0]}
+        if progress is not None:
+            progress(le, len(tok_all))
     res = {"out_bits": bf16_bits(out), "ids": ids, "weights": weights}
     if keep_intermediates:
         res["experts"] = inter
