@@ -2,7 +2,7 @@
 """moe_forward benchmark on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4] [--no-cpu-baseline]
-                    [--no-headline] [--no-upstream]
+                    [--no-headline] [--no-upstream] [--no-sweep] [--sweep-steps S]
 
 A step is one moe_forward (route, dispatch, GEMM1+SwiGLU+FP8 requant,
 GEMM2, combine) over one batch with pre-packed weights already resident in
@@ -18,7 +18,9 @@ fp32 dequant, per-expert fp32 GEMMs) on the host, on whole forwards of each
 configuration's batch (a bounded number per configuration).  Under
 "upstream", the producer of the forward's inputs (moe_router_quant: router
 GEMM + dynamic FP8 activation quantisation from bf16 hidden states) is timed
-at each configuration's T.
+at each configuration's T.  Under "reference_sweep", run_custom is timed at
+the reference benchmark's own T points with its builder's inputs
+(bench/bench_moe.py:18-20,101-118).
 
 Prints one JSON line on stdout; progress goes to stderr.  --no-headline
 times only the listed configurations (for per-configuration kernel traces)
@@ -80,6 +82,9 @@ def main() -> int:
     ap.add_argument("--no-headline", action="store_true",
                     help="time only the listed configs (no headline config 1, no summary line)")
     ap.add_argument("--no-upstream", action="store_true", help="skip the moe_router_quant timing")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the reference benchmark's own T sweep (run_custom at its builder's inputs)")
+    ap.add_argument("--sweep-steps", type=int, default=20, help="timed run_custom calls per T of the sweep")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run one plain 512 MiB device copy (the known-size reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes) and exit")
@@ -233,6 +238,7 @@ def main() -> int:
         del inp, p13, p2, args_fwd, out, ws, evs, kw
         torch.cuda.empty_cache()
 
+    sweep = [] if args.no_sweep or args.no_headline else _reference_sweep(torch, moe_layer, args.sweep_steps)
     upstream = [] if args.no_upstream or args.no_headline else [
         _time_upstream(torch, lib, dev, inputs_mod.CONFIGS[i].T, args.steps) for i in cfg_ids]
     # last: its full-power MFMA launches leave the GPU hot for what follows
@@ -300,11 +306,51 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu_baseline,
         "configs": results,
+        "reference_sweep": sweep,
         "mfma_ceiling": ceiling,
         "upstream": upstream,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+# The reference benchmark's T points and its timing loop (bench/bench_moe.py:18-20,35-46,101-118): at
+# each T, the reference builder's inputs (seed 0: U(-1,1) e4m3 activations and weights, scales
+# U(0.01, 0.11), zero bias, rsf 1.0) timed through the drop-in run_custom, 10 warm-up calls first.
+REFERENCE_T_VALUES = (1, 4, 32, 64, 256, 2048, 4096, 8192, 16384)
+
+
+def _reference_sweep(torch, moe_layer, steps: int) -> list:
+    """Latency of moe_layer.run_custom at each of the reference benchmark's T
+    values with its own builder's inputs; FLOPs counted as the reference does
+    (local routes x FLOPS_PER_ROUTE, bench/bench_moe.py:29-32,103-104)."""
+    geo = importlib.import_module("15642_moe_amd.geometry")
+    ops = moe_layer._load_custom_ops()
+    stream = torch.cuda.current_stream()
+    out = []
+    for T in REFERENCE_T_VALUES:
+        inp = moe_layer.build_moe_inputs(T=T, device="cuda")
+        routes = int(ops.route(inp["routing_logits"].to(torch.float32).contiguous(),
+                               inp["routing_bias"].to(torch.float32).contiguous(),
+                               float(inp["routed_scaling_factor"]), int(inp["local_expert_offset"]))["counts"].sum())
+        for _ in range(10):
+            moe_layer.run_custom(ops, **inp)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            moe_layer.run_custom(ops, **inp)
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / steps
+        rec = {"T": T, "local_routes": routes, "run_custom_us": round(us, 2),
+               "tflops": round(routes * geo.FLOPS_PER_ROUTE / (us * 1e-6) / 1e12, 1), "steps": steps}
+        log(f"reference sweep: {json.dumps(rec)}")
+        out.append(rec)
+        moe_layer._packed_weight_cache.clear()
+        del inp
+        torch.cuda.empty_cache()
+    return out
 
 
 def _mfma_ceiling(torch, lib, dev, capi) -> dict:
@@ -349,8 +395,8 @@ def _mfma_ceiling(torch, lib, dev, capi) -> dict:
 def _cpu_baseline(inputs_cpu: dict, cfg, gpu_us: float, budget_s: float) -> dict:
     """The oracle's restatement of reference/moe_ref.run (full fp32 dequant,
     per-expert fp32 GEMMs) on whole forwards of one configuration's batch, on
-    the host's cores: up to three forwards, or fewer when the next would run
-    past budget_s; the first is a warm-up when there are several."""
+    the host's cores: one warm-up forward, then up to three timed ones
+    (fewer only when the next would run past budget_s)."""
     import torch
 
     from oracle import moe_cpu  # CPU-baseline leg only
@@ -365,7 +411,7 @@ def _cpu_baseline(inputs_cpu: dict, cfg, gpu_us: float, budget_s: float) -> dict
         moe_cpu.forward_full_dequant(inputs_cpu)
         times.append(time.perf_counter() - t0)
         log(f"cpu baseline {cfg.name} forward {len(times)}: {times[-1]:.2f} s")
-        if len(times) >= 3 or time.perf_counter() + times[-1] > t_end:
+        if len(times) >= 4 or time.perf_counter() + times[-1] > t_end:
             break
     steady = times[1:] if len(times) > 1 else times
     us = sum(steady) / len(steady) * 1e6
@@ -373,7 +419,8 @@ def _cpu_baseline(inputs_cpu: dict, cfg, gpu_us: float, budget_s: float) -> dict
         "us": round(us, 1),
         "T": cfg.T,
         "cores": torch.get_num_threads(),
-        "sample": (f"{len(times)} full forwards of config {cfg.name}, first treated as warm-up" if len(times) > 1
+        "timed_forwards": len(steady),
+        "sample": (f"1 warm-up + {len(steady)} timed full forwards of config {cfg.name}" if len(times) > 1
                    else f"1 full forward of config {cfg.name}"),
         "gpu_speedup": round(us / gpu_us, 1),
     }

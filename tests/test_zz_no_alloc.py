@@ -2,11 +2,17 @@
 array, for callers that cannot allocate.  Its output must equal
 moe_forward's (same kernels, a caller workspace) bit for bit, on calls in a
 row whose second input is smaller than the first (the scratch keeps the
-previous call's contents), on both the decode and the prefill kernels."""
+previous call's contents), on both the decode and the prefill kernels; and
+captured into a HIP graph (torch.cuda.CUDAGraph), with and without an eager
+call first, every replay over new inputs must equal moe_forward bit for
+bit."""
 
 from __future__ import annotations
 
 import ctypes
+import subprocess
+import sys
+from pathlib import Path
 
 import pytest
 import torch
@@ -65,3 +71,27 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(cuda):
     rc = lib.moe_forward_noalloc(*([null] * 8), 1.0, 0, T, 32, null, null)
     assert rc == capi.MOE_ERR_WORKSPACE
     assert b"moe_forward_noalloc" in lib.moe_last_error()
+
+
+@pytest.mark.parametrize("T", [64, 130])
+def test_noalloc_graph_capture_after_a_call(cuda, T):
+    """T=64: decode kernels; T=130: prefill kernels.  One eager call, then
+    capture, then replays over new inputs (graph_noalloc.run_graph_case)."""
+    from graph_noalloc import run_graph_case
+
+    print(f"[graph] in-process T={T}", flush=True)
+    run_graph_case(T, warm=True)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("T", [64, 130])
+def test_noalloc_graph_capture_as_first_call(cuda, T):
+    """The capture is the process's first forward call (the scratch address
+    lookup and every forward kernel's first launch happen inside it): a
+    fresh child process runs graph_noalloc.py for this T."""
+    script = Path(__file__).resolve().with_name("graph_noalloc.py")
+    print(f"[graph] child process T={T}", flush=True)
+    res = subprocess.run([sys.executable, str(script), str(T), "0"], capture_output=True, text=True, timeout=540)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0, f"child exited {res.returncode}"
+    assert "[graph] ok" in res.stdout
