@@ -177,11 +177,26 @@ struct ActStage {
     for (int i = 0; i < NI; ++i) load_chunk(i, abase_k, ga, tid);
     load_scale(sbase_k, ga);
   }
+  // The chunks only: the item's activation scales sit in an LDS table
+  // (see store_with_scale).
+  template <int NI = G::ACH>
+  __device__ __forceinline__ void load_chunks(const uint8_t* abase_k, const GatherAddr<CT>& ga, int tid) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) load_chunk(i, abase_k, ga, tid);
+  }
   template <int NI = G::ACH>
   __device__ __forceinline__ void store(uint8_t* s_act, float2* s_scl, int b, int tid, float w0, float w1) const {
 #pragma unroll
     for (int i = 0; i < NI; ++i) store_chunk(i, s_act, b, tid);
     store_scale(s_scl, b, tid, w0, w1);
+  }
+  // store() with route tid's activation scale `a` taken from the item's LDS
+  // scale table instead of a per-K-block load.
+  template <int NI = G::ACH>
+  __device__ __forceinline__ void store_with_scale(uint8_t* s_act, float2* s_scl, int b, int tid, float a, float w0,
+                                                   float w1) {
+    sc = a;
+    store<NI>(s_act, s_scl, b, tid, w0, w1);
   }
 };
 
@@ -531,6 +546,12 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   __shared__ uint32_t s_rowoff[BM], s_soff[BM];
   __shared__ float s_rw[BM];
   __shared__ int s_single[BM];  // token of a route whose token has no other local route, else -1
+  // The item's C scales, K-block-major (s_cs[kb * BM + r]), read once per
+  // item from its contiguous C_scale rows: a per-K-block load of route r's
+  // scale (C_scale[r, kb], 64 bytes apart per route) touched a cache line per
+  // two routes, 32 lines per wave instruction for 256 useful bytes, more
+  // lines than the step's weight and activation loads together.
+  __shared__ float s_cs[IB * BM];
   __shared__ int s_tp[MAX_E_LOCAL + 1], s_cnt[MAX_E_LOCAL], s_off[MAX_E_LOCAL], s_item;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -569,9 +590,20 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
       s_rowoff[r] = (uint32_t)rr * I;
       s_soff[r] = (uint32_t)rr * IB;
     }
+    // The item's C_scale rows rb .. rb + rows - 1 (contiguous, 16 floats each)
+    // into s_cs; padding routes get 0 (their columns are never stored).
+    for (int i = tid; i < BM * IB / 4; i += G::NT) {
+      const int r = i / (IB / 4), kq = 4 * (i % (IB / 4));
+      const float4 v = r < rows ? reinterpret_cast<const float4*>(Cs + (size_t)rb * IB)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      s_cs[(kq + 0) * BM + r] = v.x;
+      s_cs[(kq + 1) * BM + r] = v.y;
+      s_cs[(kq + 2) * BM + r] = v.z;
+      s_cs[(kq + 3) * BM + r] = v.w;
+    }
     __syncthreads();
     GatherAddr<CT> ga;
     ga.bind(s_rowoff, s_soff, tid);
+    const int rs = tid < BM ? tid : 0;  // this thread's row of s_cs (threads past BM store unused slots)
 
     const uint8_t* afr = s_act + lane * 16;
     const int hb = 2 * hp + (w >> 2), t0 = 2 * (w & 3);
@@ -604,11 +636,11 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 #pragma unroll
       for (int w0 = 0; w0 < WS - 1; ++w0) wload(w0, w0);
 #pragma unroll
-      for (int a0 = 0; a0 < AS; ++a0) st[a0].template load<NI>(Cq + (size_t)a0 * BLK, Cs + a0, ga, tid);
+      for (int a0 = 0; a0 < AS; ++a0) st[a0].template load_chunks<NI>(Cq + (size_t)a0 * BLK, ga, tid);
       // the staging stores (scale x w(2hp), scale x w(2hp+1)); each wave reads
       // the component of its own H block (ascl is offset by w/4)
-      st[0].template store<NI>(s_act, s_scl, 0, tid, lane_value(ws_l, 0), lane_value(ws_l, IB));
-      st[0].template load<NI>(Cq + (size_t)AS * BLK, Cs + AS, ga, tid);
+      st[0].template store_with_scale<NI>(s_act, s_scl, 0, tid, s_cs[rs], lane_value(ws_l, 0), lane_value(ws_l, IB));
+      st[0].template load_chunks<NI>(Cq + (size_t)AS * BLK, ga, tid);
       if (tid < BM) {  // read after the K loop's barriers
         s_rw[tid] = rw_mine;
         s_single[tid] = single_mine;
@@ -626,10 +658,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
           wload(kw, (s + WS - 1) % WS);
           pipe.template step<NC>(s, acc, wf[s % WS], afr + (s & 1) * FRAG_BYTES, ascl + (s & 1) * 2 * G::NT,
                                  kb == 0);
-          st[(s + 1) % AS].template store<NI>(s_act, s_scl, (s + 1) & 1, tid, lane_value(ws_l, k1),
-                                              lane_value(ws_l, IB + k1));
+          st[(s + 1) % AS].template store_with_scale<NI>(s_act, s_scl, (s + 1) & 1, tid, s_cs[k1 * BM + rs],
+                                                         lane_value(ws_l, k1), lane_value(ws_l, IB + k1));
           __builtin_amdgcn_sched_barrier(0);
-          st[(s + 1) % AS].template load<NI>(Cq + (size_t)ka * BLK, Cs + ka, ga, tid);
+          st[(s + 1) % AS].template load_chunks<NI>(Cq + (size_t)ka * BLK, ga, tid);
         }
       }
       pipe.template drain<NC>(acc);
