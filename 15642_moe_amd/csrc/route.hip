@@ -255,8 +255,12 @@ dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T, int e_local, 
 }
 
 // Pass 2: chunk c's first slot per expert = offsets[e] + counts of chunks
-// before c (lane e sums the even chunks, lane 32 + e the odd ones), then its
-// tokens' routes.
+// before c, then its tokens' routes.  SCANNED == false: this workgroup sums
+// the counts of the chunks before its own (lane e the even chunks, lane
+// 32 + e the odd ones), a loop as long as the chunk count;  SCANNED == true
+// (large T): dispatch_scan_kernel has already replaced every chunk's counts
+// by its first slots and published counts / offsets.
+template <bool SCANNED>
 __global__ void __launch_bounds__(64)
 dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
                       int offset, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
@@ -270,21 +274,74 @@ dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restr
   int ids[TOP_K];
   float ws[TOP_K];
   const uint32_t m = load_picks(topk_ids, topk_w, t, valid, offset, e_local, ids, ws);
-  const int e = lane & (MAX_E_LOCAL - 1);
-  int pre = 0, tot = 0;
+  if constexpr (SCANNED) {
+    if (lane < MAX_E_LOCAL) s_base[lane] = chunk_counts[(size_t)c * MAX_E_LOCAL + lane];
+  } else {
+    const int e = lane & (MAX_E_LOCAL - 1);
+    int pre = 0, tot = 0;
 #pragma unroll 8
-  for (int cc = lane >> 5; cc < nchunks; cc += 2) {
-    const int v = chunk_counts[(size_t)cc * MAX_E_LOCAL + e];
-    pre += cc < c ? v : 0;
-    tot += v;
+    for (int cc = lane >> 5; cc < nchunks; cc += 2) {
+      const int v = chunk_counts[(size_t)cc * MAX_E_LOCAL + e];
+      pre += cc < c ? v : 0;
+      tot += v;
+    }
+    pre += __shfl_xor(pre, 32);
+    tot += __shfl_xor(tot, 32);
+    const int excl = expert_offsets(tot, lane, e_local, c == 0 && lane < MAX_E_LOCAL, counts, offsets);
+    if (lane < MAX_E_LOCAL) s_base[lane] = excl + pre;
   }
-  pre += __shfl_xor(pre, 32);
-  tot += __shfl_xor(tot, 32);
-  const int excl = expert_offsets(tot, lane, e_local, c == 0 && lane < MAX_E_LOCAL, counts, offsets);
-  if (lane < MAX_E_LOCAL) s_base[lane] = excl + pre;
   wave_expert_ballots(m, e_local, lane, s_bal);
   __syncthreads();
   place_wave(ids, ws, m, t, valid, offset, e_local, s_base, s_bal, lane, route_token, route_weight, token_route);
+}
+
+// Large T: one workgroup turns every chunk's per-expert counts into its
+// first slots, in place (chunk_counts[c][e] <- offsets[e] + sum of
+// chunk_counts[c'][e] over c' < c), and publishes counts / offsets, so each
+// place workgroup reads its 32 slots instead of summing all earlier chunks.
+// Thread (e, j) = (tid / 32, tid % 32) owns chunks [j*per, (j+1)*per) of
+// expert e's column: its sum, a 32-lane scan of the sums, then its chunks'
+// slots from the scanned start.
+constexpr int SCAN_THREADS = MAX_E_LOCAL * 32;
+__global__ void __launch_bounds__(SCAN_THREADS)
+dispatch_scan_kernel(int nchunks, int e_local, int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+                     int32_t* __restrict__ offsets) {
+  __shared__ int s_tot[MAX_E_LOCAL], s_off[MAX_E_LOCAL];
+  const int tid = threadIdx.x, e = tid >> 5, j = tid & 31;
+  const int per = (nchunks + 31) / 32, c0 = min(j * per, nchunks), c1 = min(c0 + per, nchunks);
+  int local = 0;
+  for (int c = c0; c < c1; ++c) local += chunk_counts[(size_t)c * MAX_E_LOCAL + e];
+  int inc = local;
+#pragma unroll
+  for (int d = 1; d < 32; d <<= 1) {
+    const int o = __shfl_up(inc, d, 32);
+    if (j >= d) inc += o;
+  }
+  if (j == 31) s_tot[e] = inc;
+  __syncthreads();
+  if (tid < MAX_E_LOCAL) {  // exclusive scan over the experts' totals (lanes 0..31 of wave 0)
+    const int tot = tid < e_local ? s_tot[tid] : 0;
+    int x = tot;
+#pragma unroll
+    for (int d = 1; d < MAX_E_LOCAL; d <<= 1) {
+      const int o = __shfl_up(x, d, MAX_E_LOCAL);
+      if (tid >= d) x += o;
+    }
+    s_off[tid] = x - tot;
+    if (tid < e_local) {
+      counts[tid] = tot;
+      offsets[tid] = x - tot;
+      if (tid == e_local - 1) offsets[e_local] = x;
+    }
+  }
+  __syncthreads();
+  int base = s_off[e] + inc - local;
+  for (int c = c0; c < c1; ++c) {
+    const size_t i = (size_t)c * MAX_E_LOCAL + e;
+    const int v = chunk_counts[i];
+    chunk_counts[i] = base;
+    base += v;
+  }
 }
 
 // out[t, :] = bf16( sum over the token's local routes, ascending expert, of Y[r, :] ),
@@ -393,6 +450,12 @@ hipError_t launch_route(const float* logits, const float* bias, float rsf, int T
 
 int dispatch_chunks(int T) { return T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1; }
 
+// Chunk counts up to which each place workgroup sums the earlier chunks
+// itself: its loop of nchunks / 2 loads per lane cost ~0.02 us per chunk
+// (dispatch 17.6 us at T = 8192), the scan kernel a third launch (23.4 us at
+// T = 8192), so the scan serves T > 16384 only, where the loop keeps growing.
+constexpr int DISPATCH_SCAN_MIN_CHUNKS = 256;
+
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream) {
@@ -401,9 +464,16 @@ hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, 
   dispatch_count_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts, queue);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
-  dispatch_place_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, chunk_counts,
-                                                                counts, offsets, route_token, route_weight,
-                                                                token_route);
+  if (nchunks <= DISPATCH_SCAN_MIN_CHUNKS) {
+    dispatch_place_kernel<false><<<nchunks, DISPATCH_CHUNK, 0, stream>>>(
+        topk_ids, topk_w, T, e_local, offset, chunk_counts, counts, offsets, route_token, route_weight, token_route);
+    return hipGetLastError();
+  }
+  dispatch_scan_kernel<<<1, SCAN_THREADS, 0, stream>>>(nchunks, e_local, chunk_counts, counts, offsets);
+  err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  dispatch_place_kernel<true><<<nchunks, DISPATCH_CHUNK, 0, stream>>>(
+      topk_ids, topk_w, T, e_local, offset, chunk_counts, counts, offsets, route_token, route_weight, token_route);
   return hipGetLastError();
 }
 
