@@ -121,6 +121,18 @@ struct GatherAddr {
     }
     soff = s_soff[tid < G::BM ? tid : 0] * 4u;
   }
+  // Rows base_row .. base_row + rows - 1 of row_bytes each (a route tile
+  // whose rows are contiguous; padding routes read row base_row).  No
+  // scale offset: such items read their scales from an LDS table.
+  __device__ __forceinline__ void bind_rows(uint32_t base_row, int rows, uint32_t row_bytes, int tid) {
+#pragma unroll
+    for (int i = 0; i < G::ACH; ++i) {
+      const int x = tid + i * G::NT;
+      const int r = (G::NCH % G::NT == 0 || x < G::NCH) ? chunk_route(x) : 0;
+      roff[i] = (base_row + (uint32_t)(r < rows ? r : 0)) * row_bytes + (uint32_t)(chunk_k(x) * 16);
+    }
+    soff = 0;
+  }
 };
 
 // A wave-uniform base plus a 32-bit per-lane byte offset.  The empty asm
@@ -380,19 +392,6 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
     int m0, rows;
     tile_routes(e, mt, s_tp, s_cnt, m0, rows);
     const int rb = s_off[e] + m0;
-    // Gate / up weight-block scales of K-block k in lane k, read before the
-    // row table so their latency overlaps its loads.
-    const float wsg_l = w13s[(size_t)(e * G1B + nb) * HB + min(lane, HB - 1)];
-    const float wsu_l = w13s[(size_t)(e * G1B + IB + nb) * HB + min(lane, HB - 1)];
-    for (int r = tid; r < BM; r += G::NT) {
-      const int tok = route_token[rb + (r < rows ? r : 0)] & ROUTE_TOKEN_MASK;
-      s_rowoff[r] = (uint32_t)tok * H;
-      s_soff[r] = tok;
-    }
-    __syncthreads();
-    GatherAddr<CT> ga;
-    ga.bind(s_rowoff, s_soff, tid);
-
     // This lane's fragment / scale addresses in LDS for route tile 0.
     const uint8_t* afr = s_act + lane * 16;
     const float* ascl = reinterpret_cast<const float*>(s_scl + (lane & 31));
@@ -421,11 +420,26 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         for (int r = 0; r < 16; ++r) acc[cc][r] = 0.0f;
       MmaPipe<NC, NSC> pipe;
 
-      // Prologue: weights of K-blocks 0..WS-2, activations of 0..AS-1 gathered,
-      // K-block 0 in LDS buffer 0 and K-block AS gathered into set 0.
+      // Prologue.  The gate / up weight-block scales (K-block k in lane k)
+      // and route tid's token, then the weights of K-blocks 0..WS-2: loads
+      // complete in issue order, so the row table waits only for the tokens
+      // while the weights are in flight through the row table's barrier.
+      // Then the activations of K-blocks 0..AS-1 are gathered, K-block 0
+      // goes to LDS buffer 0 and K-block AS is gathered into set 0.
+      const float wsg_l = w13s[(size_t)(e * G1B + nb) * HB + min(lane, HB - 1)];
+      const float wsu_l = w13s[(size_t)(e * G1B + IB + nb) * HB + min(lane, HB - 1)];
+      static_assert(BM <= G::NT, "one route per thread");
+      const int tok_mine = route_token[rb + (tid < rows ? tid : 0)] & ROUTE_TOKEN_MASK;
       ActStage<CT> st[AS];
 #pragma unroll
       for (int w0 = 0; w0 < WS - 1; ++w0) wload(w0, w0);
+      if (tid < BM) {
+        s_rowoff[tid] = (uint32_t)tok_mine * H;
+        s_soff[tid] = tok_mine;
+      }
+      __syncthreads();
+      GatherAddr<CT> ga;
+      ga.bind(s_rowoff, s_soff, tid);
 #pragma unroll
       for (int a0 = 0; a0 < AS; ++a0)
         st[a0].template load<NI>(hidden + (size_t)a0 * BLK, hscale + (size_t)a0 * T, ga, tid);
@@ -543,7 +557,6 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
   static_assert(2 * IB <= 64, "one K-block scale per lane");
   __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * NBUF * FRAG_BYTES];
   __shared__ float2 s_scl[NBUF * G::NT];
-  __shared__ uint32_t s_rowoff[BM], s_soff[BM];
   __shared__ float s_rw[BM];
   __shared__ int s_single[BM];  // token of a route whose token has no other local route, else -1
   // The item's C scales, K-block-major (s_cs[kb * BM + r]), read once per
@@ -577,32 +590,10 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
     const int m0 = mt * BM;
     const int rows = min(BM, s_cnt[e] - m0);
     const int rb = s_off[e] + m0;
-    // Route tid's weight and single-route token are read now and parked in
-    // LDS before the K loop, so the epilogue waits on no global load; the
-    // weight-block scales (H block 2hp, K-block k in lane k; H block 2hp+1 in
-    // lane IB + k) are read here too, ahead of the row table.
-    const float rw_mine = route_weight[rb + (tid < rows ? tid : 0)];
-    const int rt_mine = route_token[rb + (tid < rows ? tid : 0)];
-    const int single_mine = rt_mine < 0 ? (rt_mine & ROUTE_TOKEN_MASK) : -1;  // SINGLE_ROUTE_BIT
-    const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
-    for (int r = tid; r < BM; r += G::NT) {
-      const int rr = rb + (r < rows ? r : 0);
-      s_rowoff[r] = (uint32_t)rr * I;
-      s_soff[r] = (uint32_t)rr * IB;
-    }
-    // The item's C_scale rows rb .. rb + rows - 1 (contiguous, 16 floats each)
-    // into s_cs; padding routes get 0 (their columns are never stored).
-    for (int i = tid; i < BM * IB / 4; i += G::NT) {
-      const int r = i / (IB / 4), kq = 4 * (i % (IB / 4));
-      const float4 v = r < rows ? reinterpret_cast<const float4*>(Cs + (size_t)rb * IB)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-      s_cs[(kq + 0) * BM + r] = v.x;
-      s_cs[(kq + 1) * BM + r] = v.y;
-      s_cs[(kq + 2) * BM + r] = v.z;
-      s_cs[(kq + 3) * BM + r] = v.w;
-    }
-    __syncthreads();
+    // The route tile's C rows rb .. rb + rows - 1 are contiguous: the gather
+    // offsets follow from rb alone (padding routes read row rb).
     GatherAddr<CT> ga;
-    ga.bind(s_rowoff, s_soff, tid);
+    ga.bind_rows((uint32_t)rb, rows, (uint32_t)I, tid);
     const int rs = tid < BM ? tid : 0;  // this thread's row of s_cs (threads past BM store unused slots)
 
     const uint8_t* afr = s_act + lane * 16;
@@ -632,11 +623,45 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
         for (int r = 0; r < 16; ++r) acc[cc][r] = 0.0f;
       MmaPipe<NC, NSC> pipe;
 
+      // Item tables first, then the first weights and activations, all in
+      // flight together: loads complete in issue order, so the tables'
+      // waits below cover none of the streaming loads, and the item's first
+      // MFMAs wait for one memory latency rather than a table load's plus
+      // the weights'.  Route tid's weight and single-route token are parked
+      // in LDS before the K loop (the epilogue waits on no global load); the
+      // weight-block scales: H block 2hp, K-block k in lane k; H block 2hp+1
+      // in lane IB + k; the C_scale rows rb .. rb + rows - 1 (contiguous, 16
+      // floats each) go to s_cs K-block-major, 0 for padding routes (their
+      // columns are never stored).
+      const float rw_mine = route_weight[rb + (tid < rows ? tid : 0)];
+      const int rt_mine = route_token[rb + (tid < rows ? tid : 0)];
+      const float ws_l = w2s[(size_t)(e * HB + 2 * hp) * IB + min(lane, 2 * IB - 1)];
+      constexpr int NCS = (BM * IB / 4 + G::NT - 1) / G::NT;  // float4 of C_scale per thread
+      float4 csv[NCS];
+#pragma unroll
+      for (int j = 0; j < NCS; ++j) {
+        const int i = tid + j * G::NT;
+        const bool ok = i < BM * IB / 4 && i / (IB / 4) < rows;  // the load itself is unconditional
+        const float4 v = reinterpret_cast<const float4*>(Cs + (size_t)rb * IB)[ok ? i : 0];
+        csv[j] = ok ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
       ActStage<CT> st[AS];
 #pragma unroll
       for (int w0 = 0; w0 < WS - 1; ++w0) wload(w0, w0);
 #pragma unroll
       for (int a0 = 0; a0 < AS; ++a0) st[a0].template load_chunks<NI>(Cq + (size_t)a0 * BLK, ga, tid);
+#pragma unroll
+      for (int j = 0; j < NCS; ++j) {
+        const int i = tid + j * G::NT, r = i / (IB / 4), kq = 4 * (i % (IB / 4));
+        if (i < BM * IB / 4) {
+          s_cs[(kq + 0) * BM + r] = csv[j].x;
+          s_cs[(kq + 1) * BM + r] = csv[j].y;
+          s_cs[(kq + 2) * BM + r] = csv[j].z;
+          s_cs[(kq + 3) * BM + r] = csv[j].w;
+        }
+      }
+      const int single_mine = rt_mine < 0 ? (rt_mine & ROUTE_TOKEN_MASK) : -1;  // SINGLE_ROUTE_BIT
+      __syncthreads();  // s_cs
       // the staging stores (scale x w(2hp), scale x w(2hp+1)); each wave reads
       // the component of its own H block (ascl is offset by w/4)
       st[0].template store_with_scale<NI>(s_act, s_scl, 0, tid, s_cs[rs], lane_value(ws_l, 0), lane_value(ws_l, IB));
