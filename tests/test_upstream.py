@@ -10,6 +10,11 @@ inputs drive moe_forward to the same bits as the oracle's.
 
 from __future__ import annotations
 
+import math
+import shutil
+import subprocess
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -103,6 +108,46 @@ def test_pack_router_layout():
     assert np.array_equal(up.unpack_router(p), w)
 
 
+def _quotient_checker(tmp_path) -> Path:
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    exe = tmp_path / "quotient_exhaustive"
+    src = Path(__file__).with_name("quotient_exhaustive.c")
+    subprocess.run([gcc, "-O2", "-ffp-contract=off", str(src), "-o", str(exe), "-lm"], check=True)
+    return exe
+
+
+def test_quantiser_quotient_exhaustive(tmp_path):
+    """The quantiser divides by the block scale as reciprocal times x plus
+    one correction (upstream.hip quot).  For every finite bf16 block amax and
+    every bf16 element it bounds (1.07e9 pairs, all of the kernel's input
+    domain) the e4m3 code must equal that of the IEEE quotient x / s.  The
+    amax range is split over 8 processes of about equal work."""
+    exe = _quotient_checker(tmp_path)
+    top = 0x7F80
+    edges = [round(top * math.sqrt(i / 8)) for i in range(9)]
+    procs = [subprocess.Popen([str(exe), str(lo), str(hi)], stdout=subprocess.PIPE, text=True)
+             for lo, hi in zip(edges[:-1], edges[1:])]
+    pairs = 0
+    for p in procs:
+        out, _ = p.communicate(timeout=600)
+        assert p.returncode == 0, out
+        assert out.strip().endswith(" 0 code differences"), out
+        pairs += int(out.split(":")[1].split()[0])
+    assert pairs == sum(2 * ab + 2 for ab in range(top))  # every (amax, |x| <= amax, sign) pair
+
+
+def test_quantiser_quotient_checker_rejects_plain_reciprocal(tmp_path):
+    """Planted mistake: the quotient without its correction step, RN(x * RN(1/s)),
+    gives other codes (first found at amax 1.5234375, bf16 0x3FC3)."""
+    exe = _quotient_checker(tmp_path)
+    bad = subprocess.run([str(exe), "16323", "16324", "plain"], capture_output=True, text=True)
+    assert bad.returncode == 1 and "code differs" in bad.stdout
+    good = subprocess.run([str(exe), "16323", "16324"], capture_output=True, text=True)
+    assert good.returncode == 0, good.stdout
+
+
 # --------------------------------------------------------------------------- GPU
 def _to_dev(bits: np.ndarray, dev) -> torch.Tensor:
     return torch.from_numpy(bits.view(np.int16).copy()).to(dev).view(torch.bfloat16)
@@ -124,7 +169,7 @@ def test_pack_router_matches_oracle(ops, cuda, router):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [1, 7, 64, 100, 1000, 4096])
+@pytest.mark.parametrize("T", [1, 7, 64, 100, 1000, 4096, 4097, 6000])
 def test_router_quant_parity(ops, cuda, router, T):
     w, packed = router
     bits = _hidden_bits(T, 100 + T)
