@@ -18,8 +18,9 @@ fp32 dequant, per-expert fp32 GEMMs) on the host, on whole forwards of each
 configuration's batch (a bounded number per configuration).  Under
 "upstream", the producer of the forward's inputs (moe_router_quant: router
 GEMM + dynamic FP8 activation quantisation from bf16 hidden states) is timed
-at each configuration's T.  Under "reference_sweep", run_custom is timed at
-the reference benchmark's own T points with its builder's inputs
+at each configuration's T.  Under "reference_sweep" (and as latency-only
+"reference_T<T>" entries under "configs"), run_custom is timed at the
+reference benchmark's own T points with its builder's inputs
 (bench/bench_moe.py:18-20,101-118).
 
 Prints one JSON line on stdout; progress goes to stderr.  --no-headline
@@ -245,6 +246,11 @@ def main() -> int:
     ceiling = _mfma_ceiling(torch, lib, dev, capi)
     for rec in results.values():
         rec["stage_frac_of_mfma_ceiling"] = {k: round(v / ceiling["tflops"], 4) for k, v in rec["stage_tflops"].items()}
+    # the reference benchmark's own T points, latency only, beside the configs
+    for rec in sweep:
+        results[f"reference_T{rec['T']}"] = {
+            **rec, "latency_us": rec["run_custom_us"],
+            "workload": "reference builder inputs (moe_layer.build_moe_inputs), timed through moe_layer.run_custom"}
     if args.no_headline:
         print(json.dumps({"metric": METRIC, "configs": results, "mfma_ceiling": ceiling,
                           "cpu_baseline_per_config": cpu_runs or None}), flush=True)
