@@ -151,6 +151,21 @@ def test_routing_edge_cases(ops, cuda, T, offset, e_local, seed):
     assert np.array_equal(got["token_route"].cpu().numpy(), d["token_route"])
 
 
+def test_routing_many_ties(ops, cuda):
+    """Logits and bias from three and two levels: most biased scores tie,
+    inside a lane's four experts, across lanes and across groups, so the
+    top-8 cut falls inside runs of equal keys (taken in ascending expert
+    order) and the group ranking meets equal scores."""
+    rng = np.random.default_rng(77)
+    T = 512
+    logits = torch.from_numpy(rng.integers(0, 3, size=(T, 256)).astype(np.float32))
+    bias = torch.from_numpy((rng.integers(0, 2, size=256) * 0.5).astype(np.float32))
+    got = _gpu_route(ops, logits, bias, 2.5, 0, 32, cuda)
+    ref = routing.route(logits.numpy(), bias.numpy(), 2.5)
+    assert np.array_equal(got["topk_ids"].cpu().numpy(), ref["ids"])
+    assert np.array_equal(got["topk_w"].cpu().numpy().view(np.uint32), ref["weights"].view(np.uint32))
+
+
 def test_routing_exact_ties(ops, cuda):
     logits = torch.zeros((4, 256), dtype=torch.float32)
     logits[1, 100:140] = 1.0  # equal values straddling two groups
