@@ -73,16 +73,29 @@ __device__ __forceinline__ float row16_max(float m) {
   return m;
 }
 
-// x / s correctly rounded where the quantiser's e4m3 code can tell:
-// the reciprocal y = RN(1/s) once per block, then per element q0 = RN(x*y),
-// the exact remainder r = x - q0*s (one FMA) and q = RN(q0 + r*y)
-// (Markstein's correction step), with x's sign (the correction turns a -0
-// quotient into +0).  For every pair the quantiser can meet -- every finite
-// bf16 block amax a, s = max(RN(a/448), 1e-8), and every bf16 x with
-// |x| <= a -- e4m3_rne(clamp(q)) equals e4m3_rne(clamp(RN(x/s))); the
+// The block scale RN(m / 448) as a reciprocal product plus one FMA
+// correction (Markstein's scheme, with c = RN(1/448)): three instructions
+// where the IEEE division takes about ten.  Equal bit for bit to the IEEE
+// quotient for every finite bf16 amax m (the row maximum of bf16 elements
+// takes no other values): tests/quotient_exhaustive.c checks all of them.
+__device__ __forceinline__ float quant_scale(float m) {
+  constexpr float c = 1.0f / E4M3_MAX;
+  const float q0 = m * c;
+  return __builtin_fmaf(__builtin_fmaf(-q0, E4M3_MAX, m), c, q0);
+}
+
+// x / s where the quantiser's e4m3 code can tell: with a reciprocal y of s
+// (v_rcp_f32, documented as accurate to 1 ulp: one instruction, where the
+// correctly rounded 1/s takes about ten), q0 = RN(x*y), the exact remainder
+// r = x - q0*s (one FMA) and q = RN(q0 + r*y) (Markstein's correction
+// step), with x's sign (the correction turns a -0 quotient into +0).  For
+// every pair the quantiser can meet -- every finite bf16 block amax a, s =
+// max(RN(a/448), 1e-8), every bf16 x with |x| <= a -- and every y within
+// 1 ulp of 1/s, e4m3_rne(clamp(q)) equals e4m3_rne(clamp(RN(x/s))); the
 // quotients themselves differ only below fp32's normal range.
-// tests/quotient_exhaustive.c checks all 1.07e9 pairs.  Three operations per
-// element where the IEEE division takes about ten.
+// tests/quotient_exhaustive.c checks all 1.07e9 pairs with each of the
+// three such y.  Three operations per element where the IEEE division
+// takes about ten.
 __device__ __forceinline__ float quot(float x, float s, float y) {
   const float q0 = x * y;
   const float r = __builtin_fmaf(-q0, s, x);
@@ -227,8 +240,8 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
 #pragma unroll
       for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(f[q]));
       m = row16_max(m);
-      const float sc = fmaxf(m / E4M3_MAX, 1.0e-8f);
-      const float isc = 1.0f / sc;
+      const float sc = fmaxf(quant_scale(m), 1.0e-8f);
+      const float isc = __builtin_amdgcn_rcpf(sc);
 #pragma unroll
       for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(quot(f[q], sc, isc), -E4M3_MAX), E4M3_MAX);
       u32x2 codes;

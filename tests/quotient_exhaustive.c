@@ -1,13 +1,20 @@
-/* Exhaustive check of the quantiser's division (15642_moe_amd/csrc/upstream.hip,
- * quot): for every finite bf16 block amax a >= 0 in [lo, hi) (bf16 bit
+/* Exhaustive check of the quantiser's arithmetic (15642_moe_amd/csrc/upstream.hip,
+ * quant_scale and quot).
+ *
+ * Scale: for every finite bf16 block amax m >= 0 (every value the row
+ * maximum of bf16 elements can take), q0 = RN(m * c) with c = RN(1/448),
+ * r = fma(-q0, 448, m), s = fma(r, c, q0) must equal RN(m / 448) bit for bit.
+ *
+ * Quotient: for every finite bf16 block amax a >= 0 in [lo, hi) (bf16 bit
  * patterns) and every bf16 x with |x| <= a, both signs,
- *   s  = max(RN(a / 448), 1e-8),  y = RN(1 / s),
+ *   s  = max(RN(a / 448), 1e-8),  y = any float within 1 ulp of 1/s
+ *        (RN(1/s) and its two neighbours: the kernel takes v_rcp_f32,
+ *        documented as accurate to 1 ulp),
  *   q0 = RN(x * y),  r = fma(-q0, s, x),  q = copysign(fma(r, y, q0), x)
  * must give the same e4m3 code (RNE, after clamping to +-448) as the IEEE
  * quotient RN(x / s) that the reference rule (x / s, kernels/moe.cu:516-541)
- * and the oracle use.  Prints the pair count, the number of pairs whose
- * quotients differ in any bit and the number whose codes differ; exits 1 if
- * any code differs.  A third argument "plain" checks q = copysign(RN(x * y), x)
+ * and the oracle use.  Prints the counts; exits 1 if any scale or code
+ * differs.  A third argument "plain" checks q = copysign(RN(x * RN(1/s)), x)
  * instead (no correction step), which the checker must reject.  Build:
  * gcc -O2 -ffp-contract=off ... -lm (no contraction: every operation above is
  * rounded on its own, as the GPU code issues them). */
@@ -61,29 +68,44 @@ int main(int argc, char** argv) {
   for (int c = 0; c < 127; ++c) e4m3_value[c] = e4m3_decode(c);
   const int lo = argc > 1 ? atoi(argv[1]) : 0, hi = argc > 2 ? atoi(argv[2]) : 0x7F80;
   const int plain = argc > 3 && strcmp(argv[3], "plain") == 0;
-  long long pairs = 0, quotient_diff = 0, code_diff = 0;
+
+  long long scale_diff = 0;
+  const float c448 = 1.0f / 448.0f;
+  for (int mb = 0; mb < 0x7F80; ++mb) {
+    const float m = bf16((uint16_t)mb);
+    const float q0 = m * c448;
+    const float s = fmaf(fmaf(-q0, 448.0f, m), c448, q0);
+    if (bits(s) != bits(m / 448.0f)) {
+      if (scale_diff < 10) printf("scale differs: m=%a m/448=%a got=%a\n", m, m / 448.0f, s);
+      ++scale_diff;
+    }
+  }
+
+  long long cases = 0, code_diff = 0;
   for (int ab = lo; ab < hi && ab < 0x7F80; ++ab) {
     const float a = bf16((uint16_t)ab);
     const float s = fmaxf(a / 448.0f, 1e-8f);
-    const float y = 1.0f / s;
+    const float y_rn = 1.0f / s;
+    const float ys[3] = {nextafterf(y_rn, 0.0f), y_rn, nextafterf(y_rn, INFINITY)};
     for (int xb = 0; xb <= ab; ++xb) {
       for (int neg = 0; neg < 2; ++neg) {
         const float x = bf16((uint16_t)(xb | (neg << 15)));
-        const float ref = x / s;
-        const float q0 = x * y;
-        const float r = fmaf(-q0, s, x);
-        const float q = plain ? copysignf(q0, x) : copysignf(fmaf(r, y, q0), x);
-        ++pairs;
-        if (bits(q) == bits(ref)) continue;
-        ++quotient_diff;
-        if (e4m3_code(q) != e4m3_code(ref)) {
-          if (code_diff < 10) printf("code differs: a=%a x=%a s=%a x/s=%a q=%a\n", a, x, s, ref, q);
-          ++code_diff;
+        const int want = e4m3_code(x / s);
+        for (int k = plain ? 1 : 0; k < (plain ? 2 : 3); ++k) {
+          const float y = ys[k];
+          const float q0 = x * y;
+          const float r = fmaf(-q0, s, x);
+          const float q = plain ? copysignf(q0, x) : copysignf(fmaf(r, y, q0), x);
+          ++cases;
+          if (e4m3_code(q) != want) {
+            if (code_diff < 10) printf("code differs: a=%a x=%a s=%a y=%a x/s=%a q=%a\n", a, x, s, y, x / s, q);
+            ++code_diff;
+          }
         }
       }
     }
   }
-  printf("amax bits [%d, %d): %lld pairs, %lld quotient differences, %lld code differences\n", lo, hi, pairs,
-         quotient_diff, code_diff);
-  return code_diff != 0;
+  printf("scale: %lld differences; amax bits [%d, %d): %lld cases, %lld code differences\n", scale_diff, lo, hi,
+         cases, code_diff);
+  return scale_diff != 0 || code_diff != 0;
 }
