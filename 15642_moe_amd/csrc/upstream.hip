@@ -78,10 +78,13 @@ __device__ __forceinline__ float row16_max(float m) {
 // where the IEEE division takes about ten.  Equal bit for bit to the IEEE
 // quotient for every finite bf16 amax m (the row maximum of bf16 elements
 // takes no other values): tests/quotient_exhaustive.c checks all of them.
+// A block holding +inf keeps the IEEE result (inf; the correction would
+// give NaN), a NaN amax stays NaN.
 __device__ __forceinline__ float quant_scale(float m) {
   constexpr float c = 1.0f / E4M3_MAX;
   const float q0 = m * c;
-  return __builtin_fmaf(__builtin_fmaf(-q0, E4M3_MAX, m), c, q0);
+  const float s = __builtin_fmaf(__builtin_fmaf(-q0, E4M3_MAX, m), c, q0);
+  return m <= __FLT_MAX__ ? s : m;
 }
 
 // x / s where the quantiser's e4m3 code can tell: with a reciprocal y of s
@@ -96,6 +99,8 @@ __device__ __forceinline__ float quant_scale(float m) {
 // tests/quotient_exhaustive.c checks all 1.07e9 pairs with each of the
 // three such y.  Three operations per element where the IEEE division
 // takes about ten.
+// The caller passes s clamped to FLT_MAX: for an infinite scale (y = 0) the
+// remainder is then x and q = x * 0 = +-0, or NaN for x = +-inf, as x / inf.
 __device__ __forceinline__ float quot(float x, float s, float y) {
   const float q0 = x * y;
   const float r = __builtin_fmaf(-q0, s, x);
@@ -241,9 +246,9 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
       for (int q = 0; q < 8; ++q) m = fmaxf(m, fabsf(f[q]));
       m = row16_max(m);
       const float sc = fmaxf(quant_scale(m), 1.0e-8f);
-      const float isc = __builtin_amdgcn_rcpf(sc);
+      const float isc = __builtin_amdgcn_rcpf(sc), scf = fminf(sc, __FLT_MAX__);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(quot(f[q], sc, isc), -E4M3_MAX), E4M3_MAX);
+      for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(quot(f[q], scf, isc), -E4M3_MAX), E4M3_MAX);
       u32x2 codes;
       codes[0] = cvt2_e4m3(f[0], f[1]) | (cvt2_e4m3(f[2], f[3]) << 16);
       codes[1] = cvt2_e4m3(f[4], f[5]) | (cvt2_e4m3(f[6], f[7]) << 16);

@@ -13,11 +13,15 @@
  *   q0 = RN(x * y),  r = fma(-q0, s, x),  q = copysign(fma(r, y, q0), x)
  * must give the same e4m3 code (RNE, after clamping to +-448) as the IEEE
  * quotient RN(x / s) that the reference rule (x / s, kernels/moe.cu:516-541)
- * and the oracle use.  Prints the counts; exits 1 if any scale or code
+ * and the oracle use.  The kernel passes s clamped to FLT_MAX to the
+ * remainder FMA and guards the scale of an infinite amax; a block whose
+ * amax is +inf is checked too, against every bf16 x including +-inf and NaN,
+ * as is the scale of +inf and NaN.  Prints the counts; exits 1 if any scale or code
  * differs.  A third argument "plain" checks q = copysign(RN(x * RN(1/s)), x)
  * instead (no correction step), which the checker must reject.  Build:
  * gcc -O2 -ffp-contract=off ... -lm (no contraction: every operation above is
  * rounded on its own, as the GPU code issues them). */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -42,10 +46,10 @@ static double e4m3_decode(int c) {
   const int e = (c >> 3) & 15, m = c & 7;
   return e ? ldexp(1.0 + m / 8.0, e - 7) : ldexp(m / 8.0, -6);
 }
-/* RNE code of q clamped to +-448; ties go to the even code. */
+/* RNE code of q clamped to +-448 as the kernel clamps, fminf(fmaxf(q, -448),
+ * 448) (a NaN quotient becomes -448); ties go to the even code. */
 static int e4m3_code(float q) {
-  if (q > 448.f) q = 448.f;
-  if (q < -448.f) q = -448.f;
+  q = fminf(fmaxf(q, -448.f), 448.f);
   const int sign = signbit(q) ? 0x80 : 0;
   const double a = fabs((double)q);
   int lo = 0, hi = 126; /* e4m3_value[lo] <= a <= e4m3_value[hi] */
@@ -81,6 +85,20 @@ int main(int argc, char** argv) {
     }
   }
 
+  {
+    const float inf = INFINITY, nan = NAN;
+    const float ms[2] = {inf, nan};
+    for (int i = 0; i < 2; ++i) {  /* the kernel's guard: m <= FLT_MAX ? corrected : m */
+      const float m = ms[i], q0 = m * c448;
+      const float s = m <= FLT_MAX ? fmaf(fmaf(-q0, 448.0f, m), c448, q0) : m;
+      const float want = m / 448.0f;
+      if (!((isnan(s) && isnan(want)) || bits(s) == bits(want))) {
+        printf("scale differs for non-finite m=%a\n", m);
+        ++scale_diff;
+      }
+    }
+  }
+
   long long cases = 0, code_diff = 0;
   for (int ab = lo; ab < hi && ab < 0x7F80; ++ab) {
     const float a = bf16((uint16_t)ab);
@@ -94,7 +112,7 @@ int main(int argc, char** argv) {
         for (int k = plain ? 1 : 0; k < (plain ? 2 : 3); ++k) {
           const float y = ys[k];
           const float q0 = x * y;
-          const float r = fmaf(-q0, s, x);
+          const float r = fmaf(-q0, fminf(s, FLT_MAX), x);
           const float q = plain ? copysignf(q0, x) : copysignf(fmaf(r, y, q0), x);
           ++cases;
           if (e4m3_code(q) != want) {
@@ -102,6 +120,19 @@ int main(int argc, char** argv) {
             ++code_diff;
           }
         }
+      }
+    }
+  }
+  if (hi >= 0x7F80 && !plain) {  /* amax +inf: s = inf, y = 1/inf = 0 exactly, every bf16 x */
+    const float s = fmaxf(INFINITY / 448.0f, 1e-8f), y = 1.0f / s;
+    for (int xb = 0; xb < 0x10000; ++xb) {
+      const float x = bf16((uint16_t)xb);
+      const float q0 = x * y;
+      const float q = copysignf(fmaf(fmaf(-q0, fminf(s, FLT_MAX), x), y, q0), x);
+      ++cases;
+      if (e4m3_code(q) != e4m3_code(x / s)) {
+        if (code_diff < 10) printf("code differs: a=inf x=%a x/s=%a q=%a\n", x, x / s, q);
+        ++code_diff;
       }
     }
   }

@@ -126,9 +126,10 @@ def test_quantiser_quotient_exhaustive(tmp_path):
     quot).  tests/quotient_exhaustive.c checks the scale bit for bit for
     every finite bf16 amax.  It checks the codes for every bf16 element each
     amax bounds (1.07e9 pairs, all of the kernel's input domain) with each
-    reciprocal within 1 ulp of 1/s.  Every code must equal that of the IEEE
-    quotient x / s.  The amax range is split over 8 processes of about equal
-    work."""
+    reciprocal within 1 ulp of 1/s, and every bf16 x (infinities and NaNs
+    included) in a block whose amax is +inf.  Every code must equal that of
+    the IEEE quotient x / s.  The amax range is split over 8 processes of
+    about equal work."""
     exe = _quotient_checker(tmp_path)
     top = 0x7F80
     edges = [round(top * math.sqrt(i / 8)) for i in range(9)]
@@ -140,8 +141,9 @@ def test_quantiser_quotient_exhaustive(tmp_path):
         assert p.returncode == 0, out
         assert out.strip().endswith(" 0 code differences") and "scale: 0 differences" in out, out
         cases += int(out.split("):")[1].split()[0])
-    # every (amax, |x| <= amax, sign) pair, with three reciprocals each
-    assert cases == 3 * sum(2 * ab + 2 for ab in range(top))
+    # every (amax, |x| <= amax, sign) pair with three reciprocals each, and
+    # every bf16 x in a block whose amax is +inf
+    assert cases == 3 * sum(2 * ab + 2 for ab in range(top)) + 65536
 
 
 def test_quantiser_quotient_checker_rejects_plain_reciprocal(tmp_path):
