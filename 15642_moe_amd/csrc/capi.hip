@@ -87,14 +87,14 @@ int route_and_dispatch(const float* logits, const float* bias, float rsf, int of
                        uint8_t* ws, const size_t* off, hipStream_t st) {
   int32_t* topk_ids = reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOPK_IDS]);
   float* topk_w = reinterpret_cast<float*>(ws + off[MOE_WS_TOPK_W]);
-  MOE_TRY(hip_status(moe::launch_route(logits, bias, rsf, T, topk_ids, topk_w, st), "route_kernel launch"));
+  int32_t* queue = reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]);
+  MOE_TRY(hip_status(moe::launch_route(logits, bias, rsf, T, topk_ids, topk_w, queue, st), "route_kernel launch"));
   MOE_TRY(hip_status(moe::launch_dispatch(topk_ids, topk_w, T, e_local, offset,
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_COUNTS]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_OFFSETS]),
                                           reinterpret_cast<int32_t*>(ws + off[MOE_WS_ROUTE_TOKEN]),
                                           reinterpret_cast<float*>(ws + off[MOE_WS_ROUTE_WEIGHT]),
-                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]),
-                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_QUEUE]), st),
+                                          reinterpret_cast<int32_t*>(ws + off[MOE_WS_TOKEN_ROUTE]), queue, st),
                      "dispatch kernels launch"));
   return MOE_OK;
 }
@@ -241,7 +241,7 @@ static int forward_impl(const void* hidden, const float* hidden_scale, const voi
   const int R = (int)max_routes(T, e_local);
 
   MOE_TRY(mark(0));
-  MOE_TRY(hip_status(moe::launch_route(logits, bias, routed_scaling_factor, T, topk_ids, topk_w, st),
+  MOE_TRY(hip_status(moe::launch_route(logits, bias, routed_scaling_factor, T, topk_ids, topk_w, queue, st),
                      "route_kernel launch"));
   MOE_TRY(mark(1));
   if (T <= moe::DECODE_MAX_T) {

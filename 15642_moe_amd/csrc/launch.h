@@ -6,10 +6,14 @@
 
 namespace moe {
 
+// `queue` (may be null) = the MOE_WS_QUEUE buffer: its work-queue counters
+// and, where launch_dispatch needs them zero, its per-chunk counts are
+// cleared here.
 hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
-                        float* topk_w, hipStream_t stream);
-// Local dispatch; `queue` = the MOE_WS_QUEUE buffer: QUEUE_COUNTERS work-queue
-// counters (cleared here) followed by dispatch_chunks(T) x MAX_E_LOCAL counts.
+                        float* topk_w, int32_t* queue, hipStream_t stream);
+// Local dispatch; `queue` = the MOE_WS_QUEUE buffer (QUEUE_COUNTERS work-queue
+// counters, then dispatch_chunks(T) x MAX_E_LOCAL counts), cleared by
+// launch_route with this buffer just before.
 int dispatch_chunks(int T);
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
@@ -26,7 +30,7 @@ hipError_t launch_fill_normal_e4m3(uint8_t* out, size_t n, uint64_t seed, uint64
 
 // Prefill grouped GEMMs.  `max_routes` bounds the routes of the launch (it
 // sizes the persistent grid); `queue` = QUEUE_COUNTERS / 2 work-queue
-// counters, zero at launch (the dispatch kernel clears all QUEUE_COUNTERS).
+// counters, zero at launch (launch_route clears them).
 hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local,

@@ -3,10 +3,11 @@
 // route_kernel     : no-aux-loss DeepSeek routing, one wave64 per token
 //                    (semantics of reference/moe_ref.py:81-107; the reference
 //                    kernel is route_dispatch_kernel, kernels/moe.cu:213-329).
-// dispatch_count_kernel + dispatch_place_kernel :
+// dispatch_fused_kernel (T <= 16384), or dispatch_count_kernel +
+// dispatch_scan_kernel + dispatch_place_kernel :
 //                    deterministic token-ordered compaction of the local
-//                    (token, expert) pairs into per-expert route lists, one
-//                    wave per 64-token chunk.
+//                    (token, expert) pairs into per-expert route lists, by
+//                    64-token chunks.
 // combine_parts_kernel / combine_rows_kernel :
 //                    per-token sum of the weighted per-route expert outputs in
 //                    ascending expert order, then bf16 RNE (the reference does
@@ -49,10 +50,13 @@ __device__ __forceinline__ float dpp_f32(float x) {
 
 __global__ void __launch_bounds__(256)
 route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, float rsf, int T,
-             int32_t* __restrict__ topk_ids, float* __restrict__ topk_w) {
+             int32_t* __restrict__ topk_ids, float* __restrict__ topk_w, int32_t* __restrict__ clear, int n_clear) {
   __shared__ float s_sel[4][TOP_K];
   __shared__ int s_id[4][TOP_K];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // Words that the kernels after this one need zero (the grid has 64 threads
+  // per token, n_clear is at most 16 + T / 2).
+  if (const int i = blockIdx.x * blockDim.x + threadIdx.x; i < n_clear) clear[i] = 0;
   const int t = blockIdx.x * 4 + wave;
   const bool active = t < T;  // uniform per wave; idle waves still reach the barrier
   const int tt = active ? t : 0;
@@ -150,13 +154,15 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
 // Local dispatch: a stable counting sort of the local (token, expert) picks
 // into per-expert route lists, so route r = offsets[e] + slot with slots in
 // token order (deterministic; the reference appends in atomic order,
-// kernels/moe.cu:313-321).  Tokens come in chunks of 64, one wave each: a
-// chunk's per-expert counts are wave ballots, and a chunk's first slot per
-// expert is the expert's offset plus the counts of the chunks before it:
-// dispatch_count_kernel writes every chunk's counts and dispatch_place_kernel
-// sums those of the chunks before its own.  One wave per workgroup spreads
-// the chunks (and their scattered stores) over the CUs; a single workgroup
-// holding every chunk of T = 1024 took 16 us, all its stores on one CU.
+// kernels/moe.cu:313-321).  Tokens come in chunks of 64, one wave64 each
+// (a lane per token): a chunk's per-expert counts are wave ballots, and a
+// chunk's first slot per expert is the expert's offset plus the counts of
+// the chunks before it.  Up to 256 chunks one launch counts and places
+// (dispatch_fused_kernel); above, dispatch_count_kernel writes every chunk's
+// counts, dispatch_scan_kernel turns them into first slots and
+// dispatch_place_kernel places.  A workgroup per chunk spreads the chunks
+// (and their scattered stores) over the CUs; a single workgroup holding
+// every chunk of T = 1024 took 16 us, all its stores on one CU.
 constexpr int DISPATCH_CHUNK = 64;
 
 // Expert e's pick count among the wave's tokens (bit e of m), in lane e.
@@ -177,25 +183,22 @@ __device__ __forceinline__ void wave_expert_ballots(uint32_t m, int e_local, int
   }
 }
 
-// Writes the routes of the wave's 64 tokens (this lane: token t, local-pick
-// mask m): token_route rows start as -1; then for every expert e that a
-// token of the wave picked, the lanes that picked it take slots base[e] +
-// (lanes below with the same pick), so consecutive lanes write consecutive
-// routes (one contiguous run per expert and store) in token order.  The
-// token's routes land in token_route in ascending expert order, and
-// route_token carries SINGLE_ROUTE_BIT for a token's only local route.
-__device__ __forceinline__ void place_wave(const int* ids, const float* ws, uint32_t m, int t, bool valid, int offset,
-                                           int e_local, const int* base, const uint64_t* bal, int lane,
-                                           int32_t* __restrict__ route_token, float* __restrict__ route_weight,
-                                           int32_t* __restrict__ token_route) {
-  if (valid) {
-    int4* row = reinterpret_cast<int4*>(token_route + (size_t)t * TOP_K);
-    row[0] = make_int4(-1, -1, -1, -1);
-    row[1] = make_int4(-1, -1, -1, -1);
-  }
+// Writes the routes of local experts e_lo .. e_hi - 1 (wave-uniform) for
+// the wave's 64 tokens (this lane: token t, local-pick mask m): for every
+// such expert e that a token of the wave picked, the lanes that picked it
+// take slots base[e] + (lanes below with the same pick), so consecutive
+// lanes write consecutive routes (one contiguous run per expert and store)
+// in token order.  The token's route of e goes to position popc(m & (2^e -
+// 1)) of its token_route row (ascending expert order; the caller writes -1
+// past its last route), and route_token carries SINGLE_ROUTE_BIT for a
+// token's only local route.
+__device__ __forceinline__ void place_range(const int* ids, const float* ws, uint32_t m, int t, int offset, int e_lo,
+                                            int e_hi, const int* base, const uint64_t* bal, int lane,
+                                            int32_t* __restrict__ route_token, float* __restrict__ route_weight,
+                                            int32_t* __restrict__ token_route) {
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   const int tag = t | (__popc(m) == 1 ? SINGLE_ROUTE_BIT : 0);
-  for (int e = 0; e < e_local; ++e) {
+  for (int e = e_lo; e < e_hi; ++e) {
     const uint64_t b = bal[e];
     if (b == 0) continue;  // wave-uniform
     if ((m >> e) & 1u) {
@@ -245,54 +248,138 @@ __device__ __forceinline__ int expert_offsets(int tot, int lane, int e_local, bo
 // Pass 1: chunk c's per-expert counts into chunk_counts[c][32].
 __global__ void __launch_bounds__(64)
 dispatch_count_kernel(const int32_t* __restrict__ topk_ids, int T, int e_local, int offset,
-                      int32_t* __restrict__ chunk_counts, int32_t* __restrict__ queue) {
+                      int32_t* __restrict__ chunk_counts) {
   const int lane = threadIdx.x;
-  if (blockIdx.x == 0 && lane < QUEUE_COUNTERS) queue[lane] = 0;  // work queues of the GEMMs that follow
   const int t = blockIdx.x * DISPATCH_CHUNK + lane;
   const uint32_t m = t < T ? local_mask(topk_ids + (size_t)t * TOP_K, offset, e_local) : 0u;
   const int c = wave_expert_counts(m, e_local, lane);
   if (lane < MAX_E_LOCAL) chunk_counts[(size_t)blockIdx.x * MAX_E_LOCAL + lane] = lane < e_local ? c : 0;
 }
 
-// Pass 2: chunk c's first slot per expert = offsets[e] + counts of chunks
-// before c, then its tokens' routes.  SCANNED == false: this workgroup sums
-// the counts of the chunks before its own (lane e the even chunks, lane
-// 32 + e the odd ones), a loop as long as the chunk count;  SCANNED == true
-// (large T): dispatch_scan_kernel has already replaced every chunk's counts
-// by its first slots and published counts / offsets.
-template <bool SCANNED>
+// Pass 3: chunk c's tokens' routes, from its first slot per expert
+// (dispatch_scan_kernel has replaced every chunk's counts by its first slots
+// and published counts / offsets).
 __global__ void __launch_bounds__(64)
 dispatch_place_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
-                      int offset, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
-                      int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
+                      int offset, const int32_t* __restrict__ chunk_counts, int32_t* __restrict__ route_token,
                       float* __restrict__ route_weight, int32_t* __restrict__ token_route) {
   __shared__ int s_base[MAX_E_LOCAL];
   __shared__ uint64_t s_bal[MAX_E_LOCAL];
-  const int lane = threadIdx.x, c = blockIdx.x, nchunks = gridDim.x;
+  const int lane = threadIdx.x, c = blockIdx.x;
   const int t = c * DISPATCH_CHUNK + lane;
   const bool valid = t < T;
   int ids[TOP_K];
   float ws[TOP_K];
   const uint32_t m = load_picks(topk_ids, topk_w, t, valid, offset, e_local, ids, ws);
-  if constexpr (SCANNED) {
-    if (lane < MAX_E_LOCAL) s_base[lane] = chunk_counts[(size_t)c * MAX_E_LOCAL + lane];
-  } else {
-    const int e = lane & (MAX_E_LOCAL - 1);
-    int pre = 0, tot = 0;
+  if (lane < MAX_E_LOCAL) s_base[lane] = chunk_counts[(size_t)c * MAX_E_LOCAL + lane];
+  wave_expert_ballots(m, e_local, lane, s_bal);
+  __syncthreads();
+  if (valid) {
+    int4* row = reinterpret_cast<int4*>(token_route + (size_t)t * TOP_K);
+    row[0] = make_int4(-1, -1, -1, -1);
+    row[1] = make_int4(-1, -1, -1, -1);
+  }
+  place_range(ids, ws, m, t, offset, 0, e_local, s_base, s_bal, lane, route_token, route_weight, token_route);
+}
+
+// Count and place in one launch, for up to DISPATCH_FUSED_MAX_CHUNKS chunks:
+// one workgroup of four waves per chunk, wave w handling local experts
+// 8w .. 8w+7 (a quarter of the per-expert ballot and placement loops of one
+// wave).  Each workgroup publishes its chunk's counts as count + 1 into
+// words that the routing kernel zeroed just before, then reads every
+// chunk's words until none is zero: the value is its own ready flag, so the
+// grid meets without a shared counter or fences (one such counter, 128
+// workgroups' atomics and polls on one address, cost ~6 us at T = 8192).
+// The waiting is safe because every workgroup of the grid can be resident at
+// once (at most 256 x 4 waves, a small part of the chip): those not yet
+// running start as others' CUs free up, none of which waits on this grid.
+// The wait is bounded (DISPATCH_SPIN_LIMIT rounds, well over a second) so
+// that a broken assumption ends the kernel instead of hanging the GPU.
+constexpr int FUSED_WAVES = 4;
+constexpr int FUSED_THREADS = 64 * FUSED_WAVES;
+constexpr int FUSED_EXPERTS = MAX_E_LOCAL / FUSED_WAVES;
+constexpr int FUSED_ROWS = FUSED_THREADS / MAX_E_LOCAL;  // chunk-sum rows of the count reduction
+constexpr int DISPATCH_FUSED_MAX_CHUNKS = 256;
+constexpr int DISPATCH_SPIN_LIMIT = 1 << 20;
+
+__global__ void __launch_bounds__(FUSED_THREADS)
+dispatch_fused_kernel(const int32_t* __restrict__ topk_ids, const float* __restrict__ topk_w, int T, int e_local,
+                      int offset, int32_t* __restrict__ chunk_counts, int32_t* __restrict__ counts,
+                      int32_t* __restrict__ offsets, int32_t* __restrict__ route_token,
+                      float* __restrict__ route_weight, int32_t* __restrict__ token_route) {
+  __shared__ uint64_t s_bal[MAX_E_LOCAL];
+  __shared__ int s_pre[FUSED_ROWS][MAX_E_LOCAL], s_tot[FUSED_ROWS][MAX_E_LOCAL];
+  __shared__ int s_base[MAX_E_LOCAL];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = blockIdx.x, nchunks = gridDim.x;
+  const int t = c * DISPATCH_CHUNK + lane;
+  const bool valid = t < T;
+  int ids[TOP_K];
+  float ws[TOP_K];
+  const uint32_t m = load_picks(topk_ids, topk_w, t, valid, offset, e_local, ids, ws);
+
+  // Phase 1: ballots and counts of this wave's experts (m has no bit at or
+  // past e_local, so those experts count zero).
+  const int e0 = w * FUSED_EXPERTS;
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < FUSED_EXPERTS; ++i) {
+    const uint64_t b = __ballot((m >> (e0 + i)) & 1u);
+    if (lane == 0) s_bal[e0 + i] = b;
+    mine = lane == i ? __popcll(b) : mine;
+  }
+  if (lane < FUSED_EXPERTS)
+    __hip_atomic_store(&chunk_counts[(size_t)c * MAX_E_LOCAL + e0 + lane], mine + 1, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+
+  // Phase 2: thread (row j, expert e) sums the counts of chunks j,
+  // j + FUSED_ROWS, ...: those before this chunk and all of them; a round
+  // that meets an unwritten word is repeated whole.
+  {
+    const int e = tid & (MAX_E_LOCAL - 1), j = tid / MAX_E_LOCAL;
+    int pre, tot;
+    bool missing;
+    int spin = 0;
+    do {
+      pre = 0;
+      tot = 0;
+      missing = false;
 #pragma unroll 8
-    for (int cc = lane >> 5; cc < nchunks; cc += 2) {
-      const int v = chunk_counts[(size_t)cc * MAX_E_LOCAL + e];
-      pre += cc < c ? v : 0;
-      tot += v;
+      for (int cc = j; cc < nchunks; cc += FUSED_ROWS) {
+        const int v = __hip_atomic_load(&chunk_counts[(size_t)cc * MAX_E_LOCAL + e], __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) - 1;
+        missing |= v < 0;
+        pre += cc < c ? v : 0;
+        tot += v;
+      }
+      if (missing) __builtin_amdgcn_s_sleep(1);
+    } while (missing && ++spin < DISPATCH_SPIN_LIMIT);
+    s_pre[j][e] = pre;
+    s_tot[j][e] = tot;
+  }
+  __syncthreads();
+  if (w == 0) {
+    int pre = 0, tot = 0;
+#pragma unroll
+    for (int j = 0; j < FUSED_ROWS; ++j) {
+      pre += s_pre[j][lane & (MAX_E_LOCAL - 1)];
+      tot += s_tot[j][lane & (MAX_E_LOCAL - 1)];
     }
-    pre += __shfl_xor(pre, 32);
-    tot += __shfl_xor(tot, 32);
     const int excl = expert_offsets(tot, lane, e_local, c == 0 && lane < MAX_E_LOCAL, counts, offsets);
     if (lane < MAX_E_LOCAL) s_base[lane] = excl + pre;
   }
-  wave_expert_ballots(m, e_local, lane, s_bal);
   __syncthreads();
-  place_wave(ids, ws, m, t, valid, offset, e_local, s_base, s_bal, lane, route_token, route_weight, token_route);
+  // Each token_route entry is written once: a route by the wave of its
+  // expert, the -1 tail by wave 0.
+  if (w == 0 && valid) {
+    const int n = __popc(m);
+#pragma unroll
+    for (int p = 0; p < TOP_K; ++p)
+      if (p >= n) token_route[(size_t)t * TOP_K + p] = -1;
+  }
+  place_range(ids, ws, m, t, offset, e0, min(e0 + FUSED_EXPERTS, e_local), s_base, s_bal, lane, route_token,
+              route_weight, token_route);
 }
 
 // Large T: one workgroup turns every chunk's per-expert counts into its
@@ -441,39 +528,39 @@ combine_rows_kernel(const float* __restrict__ Y, const int32_t* __restrict__ tok
   for (int p = 0; p < COMBINE_COLS; ++p) dst[p * COMBINE_THREADS] = bf16x4(acc[p]);
 }
 
-hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
-                        float* topk_w, hipStream_t stream) {
-  if (T <= 0) return hipSuccess;
-  route_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, bias, rsf, T, topk_ids, topk_w);
-  return hipGetLastError();
-}
-
 int dispatch_chunks(int T) { return T > 0 ? (T + DISPATCH_CHUNK - 1) / DISPATCH_CHUNK : 1; }
 
-// Chunk counts up to which each place workgroup sums the earlier chunks
-// itself: its loop of nchunks / 2 loads per lane cost ~0.02 us per chunk
-// (dispatch 17.6 us at T = 8192), the scan kernel a third launch (23.4 us at
-// T = 8192), so the scan serves T > 16384 only, where the loop keeps growing.
-constexpr int DISPATCH_SCAN_MIN_CHUNKS = 256;
+hipError_t launch_route(const float* logits, const float* bias, float rsf, int T, int32_t* topk_ids,
+                        float* topk_w, int32_t* queue, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  // The GEMMs' work-queue counters, and the per-chunk counts that the fused
+  // dispatch writes as count + 1.
+  const int nchunks = dispatch_chunks(T);
+  const int n_clear =
+      queue ? QUEUE_COUNTERS + (nchunks <= DISPATCH_FUSED_MAX_CHUNKS ? nchunks * MAX_E_LOCAL : 0) : 0;
+  route_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, bias, rsf, T, topk_ids, topk_w, queue, n_clear);
+  return hipGetLastError();
+}
 
 hipError_t launch_dispatch(const int32_t* topk_ids, const float* topk_w, int T, int e_local, int offset,
                            int32_t* counts, int32_t* offsets, int32_t* route_token, float* route_weight,
                            int32_t* token_route, int32_t* queue, hipStream_t stream) {
   const int nchunks = dispatch_chunks(T);
   int32_t* chunk_counts = queue + QUEUE_COUNTERS;
-  dispatch_count_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts, queue);
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  if (nchunks <= DISPATCH_SCAN_MIN_CHUNKS) {
-    dispatch_place_kernel<false><<<nchunks, DISPATCH_CHUNK, 0, stream>>>(
-        topk_ids, topk_w, T, e_local, offset, chunk_counts, counts, offsets, route_token, route_weight, token_route);
+  if (nchunks <= DISPATCH_FUSED_MAX_CHUNKS) {
+    dispatch_fused_kernel<<<nchunks, FUSED_THREADS, 0, stream>>>(topk_ids, topk_w, T, e_local, offset, chunk_counts,
+                                                                  counts, offsets, route_token, route_weight,
+                                                                  token_route);
     return hipGetLastError();
   }
+  dispatch_count_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(topk_ids, T, e_local, offset, chunk_counts);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
   dispatch_scan_kernel<<<1, SCAN_THREADS, 0, stream>>>(nchunks, e_local, chunk_counts, counts, offsets);
   err = hipGetLastError();
   if (err != hipSuccess) return err;
-  dispatch_place_kernel<true><<<nchunks, DISPATCH_CHUNK, 0, stream>>>(
-      topk_ids, topk_w, T, e_local, offset, chunk_counts, counts, offsets, route_token, route_weight, token_route);
+  dispatch_place_kernel<<<nchunks, DISPATCH_CHUNK, 0, stream>>>(
+      topk_ids, topk_w, T, e_local, offset, chunk_counts, route_token, route_weight, token_route);
   return hipGetLastError();
 }
 

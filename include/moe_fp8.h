@@ -55,8 +55,8 @@ enum moe_ws_buffer {
                            bit 31 set are NOT written (the token's only local
                            route: its value goes straight to out_bf16)       */
   MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/64)]  work-queue counters of the
-                           prefill GEMMs (zeroed by the dispatch of every
-                           forward), then the dispatch's per-chunk counts      */
+                           prefill GEMMs, then the dispatch's per-chunk counts
+                           (zeroed by the routing kernel of every call)       */
   MOE_WS_NBUF
 };
 /* R = T * min(8, e_local) routes at most. */

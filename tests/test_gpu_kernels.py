@@ -133,10 +133,12 @@ def test_routing_bit_exact(ops, inputs_mod, cuda, idx):
 
 @pytest.mark.parametrize("T,offset,e_local,seed", [(1, 0, 32, 1), (3, 0, 32, 2), (5, -8, 32, 3), (77, 250, 32, 4),
                                                     (130, 40, 8, 5), (2049, 224, 32, 6), (64, 300, 32, 7),
+                                                    (3000, 17, 5, 11), (16384, 0, 32, 12),
                                                     (16385, 0, 32, 8), (40000, 96, 32, 9), (70001, 0, 5, 10)])
 def test_routing_edge_cases(ops, cuda, T, offset, e_local, seed):
-    """Routing and dispatch against the oracle, bit for bit; T above 16384
-    (more than 256 64-token chunks) takes the dispatch's scan kernel."""
+    """Routing and dispatch against the oracle, bit for bit.  Up to T = 16384
+    (256 64-token chunks) one launch counts and places, with a grid barrier
+    between the two; above that the count, scan and place kernels run."""
     rng = np.random.default_rng(seed)
     logits = torch.from_numpy((rng.standard_normal((T, 256)) * 2).astype(np.float32))
     bias = torch.from_numpy((rng.standard_normal(256) * 0.1).astype(np.float32))
