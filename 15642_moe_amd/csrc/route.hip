@@ -37,8 +37,8 @@ __device__ __forceinline__ int popc(uint64_t m) { return __popcll(m); }
 
 // Cross-lane moves by DPP (no LDS round trip): quad_perm [1,0,3,2] and
 // [2,3,0,1] pair lanes l ^ 1 and l ^ 2, row_half_mirror l ^ 7 within 8
-// lanes.
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141;
+// lanes, row_mirror l ^ 15 within 16.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_HALF_MIRROR = 0x141, DPP_MIRROR = 0x140;
 template <int CTRL, int ROW_MASK = 0xF>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROW_MASK, 0xF, false);
@@ -46,6 +46,27 @@ __device__ __forceinline__ uint32_t dpp_u32(uint32_t x) {
 template <int CTRL>
 __device__ __forceinline__ float dpp_f32(float x) {
   return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(x)));
+}
+
+// Wave-wide maximum (a uniform value): within each row of 16 lanes by DPP
+// (after l ^ 1, l ^ 2, l ^ 7 and l ^ 15 every lane holds its row's maximum),
+// then over the four rows by readlane.
+// The moves use 0 (the identity of max) as the old value, so each move and
+// its max fuse into one v_max_u32 with a DPP source.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t x) {
+  return max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = dpp_max_u32<DPP_XOR1>(x);
+  x = dpp_max_u32<DPP_XOR2>(x);
+  x = dpp_max_u32<DPP_HALF_MIRROR>(x);
+  x = dpp_max_u32<DPP_MIRROR>(x);
+  const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)x, 0);
+  const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)x, 16);
+  const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)x, 32);
+  const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)x, 48);
+  return max(max(r0, r1), max(r2, r3));
 }
 
 __global__ void __launch_bounds__(256)
@@ -97,36 +118,33 @@ route_kernel(const float* __restrict__ logits, const float* __restrict__ bias, f
   }
   const bool group_sel = rank < TOPK_GROUP;
 
-  // Top-8 experts of the kept groups by (value desc, index asc): the 8th
-  // largest key is found bit by bit from wave-wide ballot counts (scalar
-  // popcounts, so the loop is mostly SALU work beside four compares), then
-  // ties at that key are filled in ascending expert order.
+  // Top-8 experts of the kept groups by (value desc, index asc): eight
+  // rounds, each taking the largest remaining key and, among equal keys, the
+  // lowest expert (the lowest lane holding it, then its lowest j).  A taken
+  // key drops to 0, below every key of a kept group, so no expert is taken
+  // twice; the excluded groups' keys are 0 from the start and 4 x 32 kept
+  // experts always leave a nonzero maximum.
   uint32_t key[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) key[j] = group_sel ? order_key(v[j]) : 0u;
-  uint32_t thr = 0;
-  for (int bit = 31; bit >= 0; --bit) {
-    const uint32_t cand = thr | (1u << bit);
-    int cnt = 0;
+  bool sel[4] = {false, false, false, false};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) cnt += popc(__ballot(key[j] >= cand));
-    if (cnt >= TOP_K) thr = cand;
+  for (int r = 0; r < TOP_K; ++r) {
+    const uint32_t mx = wave_max_u32(max(max(key[0], key[1]), max(key[2], key[3])));
+    bool hit[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hit[j] = key[j] == mx;
+    const int win = __builtin_ctzll(__ballot(hit[0] || hit[1] || hit[2] || hit[3]));
+    bool left = lane == win;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool take = left && hit[j];
+      sel[j] = sel[j] || take;
+      key[j] = take ? 0u : key[j];
+      left = left && !take;
+    }
   }
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  int n_gt = 0, eq_seen = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    n_gt += popc(__ballot(key[j] > thr));
-    eq_seen += popc(__ballot(key[j] == thr) & below);
-  }
-  const int need = TOP_K - n_gt;
-  bool sel[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool eq = key[j] == thr;
-    sel[j] = key[j] > thr || (eq && eq_seen < need);
-    eq_seen += eq ? 1 : 0;
-  }
   // Position in ascending expert order = selected experts below this one.
   int pos = 0;
 #pragma unroll
