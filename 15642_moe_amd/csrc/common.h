@@ -102,10 +102,13 @@ __device__ __forceinline__ void store_out_bf16x4(uint16_t* dst, float4 v) {
   *reinterpret_cast<uint2*>(dst) = o;
 }
 
-// Two floats -> two e4m3 bytes (low half of the result), hardware
-// v_cvt_pk_fp8_f32: RNE, non-saturating; callers clamp to +-448 first.
-__device__ __forceinline__ uint32_t cvt2_e4m3(float a, float b) {
-  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xFFFFu;
+// Four floats -> four e4m3 bytes (a in the low byte), hardware
+// v_cvt_pk_fp8_f32: RNE, non-saturating; callers clamp to +-448 first.  The
+// second conversion writes the high half of the first one's register (word
+// select), so the pair needs no mask, shift or OR.
+__device__ __forceinline__ uint32_t cvt4_e4m3(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
 }
 
 // Flag in route_token: the route is its token's only local route (the GEMM2

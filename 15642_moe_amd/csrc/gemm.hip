@@ -227,8 +227,8 @@ quant_kernel(const float* __restrict__ Cf, const int32_t* __restrict__ offsets, 
     const float sc = fmaxf(m / E4M3_MAX, 1.0e-8f);
     auto q = [&](float x) { return fminf(fmaxf(x / sc, -E4M3_MAX), E4M3_MAX); };
     uint2 o;
-    o.x = cvt2_e4m3(q(a.x), q(a.y)) | (cvt2_e4m3(q(a.z), q(a.w)) << 16);
-    o.y = cvt2_e4m3(q(b.x), q(b.y)) | (cvt2_e4m3(q(b.z), q(b.w)) << 16);
+    o.x = cvt4_e4m3(q(a.x), q(a.y), q(a.z), q(a.w));
+    o.y = cvt4_e4m3(q(b.x), q(b.y), q(b.z), q(b.w));
     *reinterpret_cast<uint2*>(Cq + (size_t)r * I + blk * BLK + sub * 8) = o;
     if (sub == 0) Cs[(size_t)r * IB + blk] = sc;
   }

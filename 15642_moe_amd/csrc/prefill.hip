@@ -515,7 +515,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
             float v[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = fminf(fmaxf(acc[cc][4 * hq + i] * isc, -E4M3_MAX), E4M3_MAX);
-            *reinterpret_cast<uint32_t*>(crow + 8 * hq) = cvt2_e4m3(v[0], v[1]) | (cvt2_e4m3(v[2], v[3]) << 16);
+            *reinterpret_cast<uint32_t*>(crow + 8 * hq) = cvt4_e4m3(v[0], v[1], v[2], v[3]);
           }
           if (w == 0 && lane < 32) Cs[(size_t)(rb + row) * IB + nb] = sc;
         }

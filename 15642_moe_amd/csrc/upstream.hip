@@ -60,17 +60,22 @@ __device__ __forceinline__ float bf16_lo(uint32_t u) { return __builtin_bit_cast
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __builtin_bit_cast(float, u & 0xFFFF0000u); }
 
 // max over the 16 lanes of a row (DPP: quad permutes, then rotations by 4
-// and 8 within the row), no LDS round trip.
+// and 8 within the row), no LDS round trip.  The values are absolute values
+// and never NaN (the lane's own maximum drops NaN inputs), and for such
+// floats the unsigned order of the bits is the float order: an integer max
+// with the DPP source fused in is one instruction per step, where the float
+// max also quiets its inputs.
 template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t v) {
+  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false));
 }
 __device__ __forceinline__ float row16_max(float m) {
-  m = fmaxf(m, dpp_f<0xB1>(m));   // quad_perm [1,0,3,2]
-  m = fmaxf(m, dpp_f<0x4E>(m));   // quad_perm [2,3,0,1]
-  m = fmaxf(m, dpp_f<0x124>(m));  // row_ror:4
-  m = fmaxf(m, dpp_f<0x128>(m));  // row_ror:8
-  return m;
+  uint32_t b = __builtin_bit_cast(uint32_t, m);
+  b = dpp_max_u32<0xB1>(b);   // quad_perm [1,0,3,2]
+  b = dpp_max_u32<0x4E>(b);   // quad_perm [2,3,0,1]
+  b = dpp_max_u32<0x124>(b);  // row_ror:4
+  b = dpp_max_u32<0x128>(b);  // row_ror:8
+  return __builtin_bit_cast(float, b);
 }
 
 // The block scale RN(m / 448) as a reciprocal product plus one FMA
@@ -250,8 +255,8 @@ router_quant_kernel(const uint8_t* __restrict__ hidden, const uint8_t* __restric
 #pragma unroll
       for (int q = 0; q < 8; ++q) f[q] = fminf(fmaxf(quot(f[q], scf, isc), -E4M3_MAX), E4M3_MAX);
       u32x2 codes;
-      codes[0] = cvt2_e4m3(f[0], f[1]) | (cvt2_e4m3(f[2], f[3]) << 16);
-      codes[1] = cvt2_e4m3(f[4], f[5]) | (cvt2_e4m3(f[6], f[7]) << 16);
+      codes[0] = cvt4_e4m3(f[0], f[1], f[2], f[3]);
+      codes[1] = cvt4_e4m3(f[4], f[5], f[6], f[7]);
       gstore2(qoff, codes, hq + (size_t)kb * BLK);
       if ((tid & 15) == 0) s_qs[kb - kb0][tid >> 4] = sc;
     }
