@@ -25,9 +25,10 @@ constexpr int MAX_E_LOCAL = 32;    // dispatch uses a 32-bit local-expert mask p
 constexpr float E4M3_MAX = 448.0f;
 // Largest token count served by the decode kernels (dispatch fused into GEMM1).
 constexpr int DECODE_MAX_T = 128;
-// Work-queue counters of the prefill GEMMs: one per XCD for each of the two.
+// Work-queue words of the prefill GEMMs, for each of the two: a claim
+// counter per XCD, then a mask of the XCD segments found drained.
 constexpr int XCDS = 8;
-constexpr int QUEUE_COUNTERS = 2 * XCDS;
+constexpr int QUEUE_COUNTERS = 2 * (XCDS + 1);
 
 // One MFMA operand tile: 16 rows x 128 K-bytes = 2 KB.  Lane l holds row
 // (l % 16) and K-bytes [32*(l/16), 32*(l/16)+32) as 8 dwords.  This is the

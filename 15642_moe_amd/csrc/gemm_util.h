@@ -127,6 +127,35 @@ __device__ __forceinline__ void decode_work(int L, int nblk, int e_local, const 
   }
 }
 
+// Item claims of a persistent prefill workgroup (thread 0's state).  The
+// logical items 0 .. n_work-1 are cut into nq equal contiguous segments, one
+// per XCD queue; a workgroup of XCD q drains segment q first, then takes
+// items from the other segments (q+1, q+2, ... mod nq), so no XCD's CUs idle
+// while another XCD still has items waiting.  queue[x] counts the claims on
+// segment x (a claim at or past its end finds it drained); bit x of
+// queue[XCDS] is set by every workgroup that finds segment x drained, and
+// the returned mask lets it skip the segments others found drained.  next()
+// marks one more segment per failed claim, so it ends after at most nq
+// rounds, returning n_work once every segment is drained: a workgroup whose
+// own segment runs dry when all others have too exits after one atomic.
+struct ItemQueue {
+  int nq, n_work, cur, claimed;
+  __device__ __forceinline__ int seg_lo(int x) const { return (int)((long long)n_work * x / nq); }
+  __device__ __forceinline__ void claim(int32_t* queue) { claimed = atomicAdd(&queue[cur], 1); }
+  __device__ __forceinline__ int next(int32_t* queue) {
+    const unsigned all = (1u << nq) - 1u;
+    for (;;) {
+      const int L = seg_lo(cur) + claimed;
+      if (L < seg_lo(cur + 1)) return L;
+      const unsigned m = atomicOr(reinterpret_cast<unsigned*>(&queue[XCDS]), 1u << cur) | (1u << cur);
+      if ((m & all) == all) return n_work;
+      do cur = cur + 1 == nq ? 0 : cur + 1;
+      while ((m >> cur) & 1u);
+      claim(queue);
+    }
+  }
+};
+
 // Routes of route tile mt of expert e: [m0, m0 + rows).  The expert's
 // 32-route pairs of MFMA fragments, ceil(count / 32), are dealt evenly over
 // its s_tp[e+1] - s_tp[e] tiles (each gets floor or ceil of the share, at

@@ -30,7 +30,8 @@ hipError_t launch_fill_normal_e4m3(uint8_t* out, size_t n, uint64_t seed, uint64
 
 // Prefill grouped GEMMs.  `max_routes` bounds the routes of the launch (it
 // sizes the persistent grid); `queue` = QUEUE_COUNTERS / 2 work-queue
-// counters, zero at launch (launch_route clears them).
+// words (XCDS claim counters and a drained-segment mask), zero at launch
+// (launch_route clears them).
 hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const uint8_t* w13p,
                          const float* w13_scale, const int32_t* counts, const int32_t* offsets,
                          const int32_t* route_token, uint8_t* Cq, float* Cs, int T, int e_local,

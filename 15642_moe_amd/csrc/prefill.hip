@@ -338,11 +338,10 @@ __device__ __forceinline__ void with_tile_count(int ncc, F&& f) {
 // XCD p % 8).  They take the segment's items in order from counter q, so the
 // items that share an expert's weight block or a route tile's activations
 // run on one XCD (one L2) at about the same time, and pulling items evens
-// out their unequal times inside the XCD.
+// out their unequal times inside the XCD.  A workgroup whose segment is
+// drained takes the other segments' remaining items (ItemQueue), which
+// evens out the XCDs' unequal totals.
 
-// Per-lane D-register rows of a 32x32 tile: register r of lane l is row
-// 8*(r/4) + 4*(l/32) + r%4.
-__device__ __forceinline__ int d_row(int r, int lane) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
 // ---------------------------------------------------------------------------
 // Stage 1.  Item (e, nb, mt): W13 rows of I-block nb x the mt-th route tile
@@ -373,20 +372,19 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
 
   const int nq = min(XCDS, (int)gridDim.x), q = blockIdx.x % nq;
   const int n_work = s_tp[e_local] * IB;
-  const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
   const uint32_t alane = a_lane_offset(lane);
 
   // Thread 0 takes the next item from the queue as soon as the current
   // item's K loop is done, so the atomic's round trip runs under the
   // epilogue (taken any earlier, the claim would hold an item back from a
   // workgroup that frees up first).
-  int claimed = 0;
-  if (tid == 0) claimed = atomicAdd(&queue[q], 1);
+  ItemQueue iq{nq, n_work, q, 0};
+  if (tid == 0) iq.claim(queue);
   for (;;) {
-    if (tid == 0) s_item = seg_lo + claimed;
+    if (tid == 0) s_item = iq.next(queue);
     __syncthreads();
     const int L = __builtin_amdgcn_readfirstlane(s_item);
-    if (L >= seg_hi) break;
+    if (L >= n_work) break;
     int e, nb, mt;
     decode_work(L, IB, e_local, s_tp, e, nb, mt);
     int m0, rows;
@@ -468,7 +466,7 @@ stage1_tile_kernel(const uint8_t* __restrict__ hidden, const float* __restrict__
         }
       }
       pipe.template drain<NC>(acc);
-      if (tid == 0) claimed = atomicAdd(&queue[q], 1);
+      if (tid == 0) iq.claim(queue);
 
       // SwiGLU (silu on the up rows, D registers 8-15, times the gate rows in
       // registers 0-7 of the same lane), and below the requant, with hardware
@@ -573,16 +571,15 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 
   const int nq = min(XCDS, (int)gridDim.x), q = blockIdx.x % nq;
   const int n_work = s_tp[e_local] * NHP;
-  const int seg_lo = (int)((long long)n_work * q / nq), seg_hi = (int)((long long)n_work * (q + 1) / nq);
   const uint32_t alane = a_lane_offset(lane);
 
-  int claimed = 0;
-  if (tid == 0) claimed = atomicAdd(&queue[q], 1);
+  ItemQueue iq{nq, n_work, q, 0};
+  if (tid == 0) iq.claim(queue);
   for (;;) {
-    if (tid == 0) s_item = seg_lo + claimed;
+    if (tid == 0) s_item = iq.next(queue);
     __syncthreads();
     const int L = __builtin_amdgcn_readfirstlane(s_item);
-    if (L >= seg_hi) break;
+    if (L >= n_work) break;
     int e, hp, mt;
     decode_work(L, NHP, e_local, s_tp, e, hp, mt);
     // Route tiles in order, the last one partial: GEMM2 measured faster this
@@ -690,7 +687,7 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
         }
       }
       pipe.template drain<NC>(acc);
-      if (tid == 0) claimed = atomicAdd(&queue[q], 1);
+      if (tid == 0) iq.claim(queue);
 
       // Lane l holds route cc*32 + l%32 and the wave's H rows 8*j + 4*(l/32)
       // + 0..3 (registers 4j..4j+3), i.e. the item's output columns 32w +

@@ -54,7 +54,7 @@ enum moe_ws_buffer {
                            rows of routes whose MOE_WS_ROUTE_TOKEN entry has
                            bit 31 set are NOT written (the token's only local
                            route: its value goes straight to out_bf16)       */
-  MOE_WS_QUEUE,         /* int32 [16 + 32*ceil(T/64)]  work-queue counters of the
+  MOE_WS_QUEUE,         /* int32 [18 + 32*ceil(T/64)]  work-queue words of the
                            prefill GEMMs, then the dispatch's per-chunk counts
                            (zeroed by the routing kernel of every call)       */
   MOE_WS_NBUF
