@@ -34,6 +34,12 @@ namespace moe {
 // exit at once.
 // ---------------------------------------------------------------------------
 
+// Lane k's value of v (k wave-uniform): the weight-block scales sit one
+// K-block per lane for the whole item.
+__device__ __forceinline__ float lane_value(float v, int k) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), k));
+}
+
 __device__ __forceinline__ void decode_map(int p, int nslice, int& e, int& slice) {
   e = p / nslice;
   slice = p - e * nslice;
@@ -124,6 +130,12 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
   const uint8_t* wp = w13p + (size_t)(e * IB + nb) * W13_SLAB_BYTES + (size_t)(2 * pj) * TILE_BYTES;
   const float* wsg_p = w13s + (size_t)(e * G1B + nb) * HB;
   const float* wsu_p = w13s + (size_t)(e * G1B + IB + nb) * HB;
+  // The gate / up weight-block scales, K-block k in lane k, read once: the
+  // asm statement takes them as inputs (so the compiler waits for these two
+  // loads here, before any ring load is in flight) and hands the K loop
+  // values with no load pending.
+  float sg_l = wsg_p[lane < HB ? lane : HB - 1], su_l = wsu_p[lane < HB ? lane : HB - 1];
+  __asm__ volatile("" : "+v"(sg_l), "+v"(su_l));
   // FR 16-route fragments per pass over the weight tiles: an expert with
   // more routes than one fragment streams its tiles once per FR fragments.
   for (int m0 = 0; m0 < my_cnt; m0 += BM * FR) {
@@ -139,10 +151,12 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
     }
     const uint32_t wvoff = (uint32_t)lane * 16;
     // loads per K-block: 2 weight tiles x 2 halves, per fragment 2
-    // activation halves and the activation scale, the two weight-block scales
-    constexpr int LPK = 4 * NPW + 3 * FR + 2;
+    // activation halves and the activation scale; all NR K-blocks' loads are
+    // in flight when a step issues its K-block, and vmcnt counts to 63
+    constexpr int LPK = 4 * NPW + 3 * FR;
+    static_assert(LPK * NR <= 63, "the ring's loads must fit the vmcnt counter");
     u32x4 wgl[NR][NPW], wgh[NR][NPW], wul[NR][NPW], wuh[NR][NPW], bl[NR][FR], bh[NR][FR];
-    float as[NR][FR], sg[NR], su[NR];
+    float as[NR][FR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W13_KB_BYTES;
 #pragma unroll
@@ -155,9 +169,8 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         gload2_adj(bl[sl][f], bh[sl][f], avoff[f], hidden + (size_t)kb * BLK);
         gload1(as[sl][f], svoff[f], hscale + (size_t)kb * T);
       }
-      gload1(sg[sl], 0u, wsg_p + kb);
-      gload1(su[sl], 0u, wsu_p + kb);
     };
+    wait_vm<0>();  // the ring starts from an empty vmcnt queue: its waits count only its own loads
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
     v4f accg[FR][NPW], accu[FR][NPW];
@@ -176,14 +189,14 @@ stage1_decode_kernel(const int32_t* __restrict__ topk_ids, const float* __restri
         for (int p = 0; p < NPW; ++p) __asm__ volatile("" : "+v"(wgl[sl][p]), "+v"(wgh[sl][p]), "+v"(wul[sl][p]), "+v"(wuh[sl][p]));
 #pragma unroll
         for (int f = 0; f < FR; ++f) __asm__ volatile("" : "+v"(bl[sl][f]), "+v"(bh[sl][f]), "+v"(as[sl][f]));
-        __asm__ volatile("" : "+v"(sg[sl]), "+v"(su[sl]));
+        const float sgk = lane_value(sg_l, kb), suk = lane_value(su_l, kb);
 #pragma unroll
         for (int f = 0; f < FR; ++f) {
           const v8i bq = frag(bl[sl][f], bh[sl][f]);
 #pragma unroll
           for (int p = 0; p < NPW; ++p) {
-            accg[f][p] += mfma_16x16x128_fp8(frag(wgl[sl][p], wgh[sl][p]), bq, zero4) * (as[sl][f] * sg[sl]);
-            accu[f][p] += mfma_16x16x128_fp8(frag(wul[sl][p], wuh[sl][p]), bq, zero4) * (as[sl][f] * su[sl]);
+            accg[f][p] += mfma_16x16x128_fp8(frag(wgl[sl][p], wgh[sl][p]), bq, zero4) * (as[sl][f] * sgk);
+            accu[f][p] += mfma_16x16x128_fp8(frag(wul[sl][p], wuh[sl][p]), bq, zero4) * (as[sl][f] * suk);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -255,6 +268,9 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
   const int hb = q >> 1, t0 = 4 * (q & 1);
   const uint8_t* wp = w2p + (size_t)(e * HB + hb) * W2_SLAB_BYTES + (size_t)t0 * TILE_BYTES;
   const float* ws_p = w2s + (size_t)(e * HB + hb) * IB;
+  // The weight-block scales, K-block k in lane k, read once (as in stage 1).
+  float sw_l = ws_p[lane < IB ? lane : IB - 1];
+  __asm__ volatile("" : "+v"(sw_l));
   const v4f zero4 = {0.f, 0.f, 0.f, 0.f};
   const int col = lane & 15;
 
@@ -272,10 +288,11 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
     }
     const uint32_t wvoff = (uint32_t)lane * 16;
     // 4 weight tiles x 2 halves, per fragment 2 activation halves and its C
-    // scale, the weight-block scale
-    constexpr int LPK = 9 + 3 * FR;
+    // scale (all NR K-blocks in flight at once, within vmcnt's 63)
+    constexpr int LPK = 8 + 3 * FR;
+    static_assert(LPK * NR <= 63, "the ring's loads must fit the vmcnt counter");
     u32x4 wl[NR][4], wh[NR][4], bl[NR][FR], bh[NR][FR];
-    float as[NR][FR], sw[NR];
+    float as[NR][FR];
     auto issue = [&](int kb, int sl) {
       const uint8_t* pw = wp + (size_t)kb * W2_KB_BYTES;
 #pragma unroll
@@ -285,8 +302,8 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
         gload2_adj(bl[sl][f], bh[sl][f], avoff[f], Cq + (size_t)kb * BLK);
         gload1(as[sl][f], svoff[f], Cs + kb);
       }
-      gload1(sw[sl], 0u, ws_p + kb);
     };
+    wait_vm<0>();  // the ring starts from an empty vmcnt queue: its waits count only its own loads
 #pragma unroll
     for (int sl = 0; sl < NR - 1; ++sl) issue(sl, sl);
     v4f acc[FR][4];
@@ -302,12 +319,12 @@ stage2_decode_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ C
         issue(min(kb + NR - 1, IB - 1), (sl + NR - 1) % NR);  // branch-free, clamped
         wait_vm<LPK * (NR - 1)>();
         __asm__ volatile("" : "+v"(wl[sl][0]), "+v"(wh[sl][0]), "+v"(wl[sl][1]), "+v"(wh[sl][1]), "+v"(wl[sl][2]),
-                         "+v"(wh[sl][2]), "+v"(wl[sl][3]), "+v"(wh[sl][3]), "+v"(sw[sl]));
+                         "+v"(wh[sl][2]), "+v"(wl[sl][3]), "+v"(wh[sl][3]));
 #pragma unroll
         for (int f = 0; f < FR; ++f) __asm__ volatile("" : "+v"(bl[sl][f]), "+v"(bh[sl][f]), "+v"(as[sl][f]));
 #pragma unroll
         for (int f = 0; f < FR; ++f) {
-          const float sc = as[sl][f] * sw[sl];
+          const float sc = as[sl][f] * lane_value(sw_l, kb);
           const v8i bq = frag(bl[sl][f], bh[sl][f]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {

@@ -27,9 +27,11 @@ __device__ __forceinline__ v8i frag(const u32x4& lo, const u32x4& hi) {
 // the ones it needs, whereas the compiler's own count at the unrolled loop's
 // entry collapses the ring for one K-block in each pass.  The registers of
 // the K-block then pass through an empty asm, which orders every use after
-// the wait.  Uniform values (weight-block scales) are loaded the same way
-// rather than by scalar loads, whose waits would cover every outstanding
-// load.
+// the wait.  vmcnt is a 6-bit count, so a ring keeps at most 63 loads in
+// flight (all NR K-blocks' loads, counted when a step issues its K-block)
+// and starts from an empty queue (an explicit vmcnt(0) before its first
+// loads); the weight-block scales are read once per item, K-block k in lane
+// k, rather than travelling in the ring.
 // The weight tiles' loads are non-temporal (nt): each weight byte is read
 // once per launch, and streaming it past the caches took the decode GEMMs
 // from 95 + 49 to 86 + 46 us at T=64.

@@ -11,7 +11,9 @@ for gfx950, finds each kernel whose body holds a vector load between
 kernel's control flow (branches and loop back-edges, whatever order the
 compiler lays the blocks out in), between such a load and the
 `s_waitcnt vmcnt` that retires it, no other instruction may read or write
-the load's destination registers.
+the load's destination registers; and no such load may, on any path, be
+issued with more vector-memory instructions in flight than the 6-bit vmcnt
+counter holds (63), since the explicit waits count on it.
 """
 
 from __future__ import annotations
@@ -48,7 +50,8 @@ LABEL_RE = re.compile(r"^(\.LBB\w+):")
 BRANCH_RE = re.compile(r"^(s_branch|s_cbranch_\w+)\s+(\.LBB\w+)")
 END_RE = re.compile(r"^(s_endpgm|s_setpc_b64|s_trap)\b")
 WAIT_RE = re.compile(r"s_waitcnt\b.*vmcnt\((\d+)\)")
-MAX_QUEUE = 72  # vmcnt counts to 63; older entries fold into the last position
+VMCNT_MAX = 63  # gfx950's vmcnt field is 6 bits
+MAX_QUEUE = 72  # older entries fold into the last position
 
 
 def _instructions(lines: list[str]):
@@ -135,6 +138,9 @@ def _transfer(state: tuple, block, problems=None) -> tuple:
         if VMEM_RE.match(ins):
             lm = LOAD_RE.match(ins)
             state = (frozenset(_regs(lm.group(2))) if (lm and in_asm) else frozenset(),) + state
+            if problems is not None and lm and in_asm and len(state) > VMCNT_MAX:
+                problems.append(f"line {i}: {ins} may be the {len(state)}th vector-memory instruction in "
+                                f"flight: vmcnt counts to {VMCNT_MAX}, so the waits that follow under-count")
             if len(state) > MAX_QUEUE:
                 state = state[:MAX_QUEUE - 1] + (frozenset().union(*state[MAX_QUEUE - 1:]),)
     return state
@@ -245,6 +251,19 @@ def test_checker_flags_a_moved_destination():
     # does not select one, an asm load under any kernel name does
     assert has_asm_load(bad) and has_asm_load(good)
     assert not has_asm_load(["global_load_dwordx4 v[0:3], v248, s[16:17]", "s_waitcnt vmcnt(0)"])
+
+
+def test_checker_flags_more_loads_in_flight_than_vmcnt_holds():
+    """A ring that issues its next K-block's loads while NR-1 K-blocks are
+    still in flight must keep all of them within vmcnt's 63: 8 K-blocks of 9
+    loads (72) are flagged, 8 of 7 (56) are not."""
+    def ring(lpk, nr):
+        lines = []
+        for k in range(lpk * nr):
+            lines += [";;#ASMSTART", f"global_load_dword v{k % 200}, v248, s[16:17]", ";;#ASMEND"]
+        return lines + [f"s_waitcnt vmcnt({lpk * (nr - 1)})", "s_endpgm"]
+    assert any("vmcnt counts to 63" in p for p in check_kernel(ring(9, 8)))
+    assert not check_kernel(ring(7, 8))
 
 
 def test_checker_follows_control_flow():

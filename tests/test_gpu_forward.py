@@ -325,11 +325,11 @@ def test_forward_partial_offset(ops, inputs_mod, cuda, packed_cache):
 
 
 # ---------------------------------------------------------------------------- reference builder
-@pytest.mark.parametrize("T", [1, 4, 32, 64, 256])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 32, 64, 256])
 def test_reference_builder_distributions(T, cuda):
     """The reference's own T sweep (tests/test_moe.py:18) at its builder's
     distributions, where its 1e-2/2e-2 tolerance is meaningful, through the
-    drop-in moe_layer.run_custom path."""
+    drop-in moe_layer.run_custom path (plus T=2 and 3)."""
     from conftest import pkg
 
     layer = pkg("moe_layer")
