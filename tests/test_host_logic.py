@@ -156,3 +156,69 @@ def test_geometry_matches_kernel_constants():
     for name, value in (("DECODE_MAX_T", geo.DECODE_MAX_T), ("MAX_E_LOCAL", geo.MAX_E_LOCAL)):
         m = re.search(rf"constexpr int {name} = (\d+);", common)
         assert m and int(m.group(1)) == value, name
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_item_queue_protocol_claims_every_item_once(seed):
+    """The prefill GEMMs' work distribution (gemm_util.h ItemQueue), played
+    as its atomics under random interleavings of the workgroups: per-XCD
+    claim counters over nq contiguous segments, a workgroup stealing from
+    the next undrained segment once its own is drained, and a drained-mask
+    word whose atomicOr result lets it skip segments others found drained.
+    Every item must be taken exactly once, and each workgroup must stop
+    after at most nq claims beyond the items it takes."""
+    rng = np.random.default_rng(seed)
+    nq = int(rng.integers(1, 9))
+    n_work = int(rng.choice([0, 1, 5, nq, 37, 256, 1000]))
+    n_wg = int(rng.integers(1, 64))
+    counters = [0] * nq
+    mask = 0
+    seg = [n_work * x // nq for x in range(nq + 1)]
+
+    def workgroup(q):
+        nonlocal mask
+        cur, claims = q % nq, 0
+
+        def claim():
+            nonlocal claims
+            claims += 1
+            c = counters[cur]
+            counters[cur] += 1
+            return c
+        claimed = claim()
+        yield None  # the atomic's round trip: other workgroups run here
+        while True:
+            L = seg[cur] + claimed
+            if L < seg[cur + 1]:
+                yield ("item", L, claims)
+                claimed = claim()
+                yield None
+                continue
+            old = mask
+            mask |= 1 << cur
+            m = old | (1 << cur)
+            yield None
+            if m & ((1 << nq) - 1) == (1 << nq) - 1:
+                yield ("done", None, claims)
+                return
+            cur = (cur + 1) % nq
+            while (m >> cur) & 1:
+                cur = (cur + 1) % nq
+            claimed = claim()
+            yield None
+
+    live = {p: workgroup(p) for p in range(n_wg)}
+    taken, items_of = [], {p: 0 for p in range(n_wg)}
+    while live:
+        p = list(live)[int(rng.integers(len(live)))]
+        ev = next(live[p])
+        if ev is None:
+            continue
+        kind, L, claims = ev
+        if kind == "item":
+            taken.append(L)
+            items_of[p] += 1
+        else:
+            assert claims <= items_of[p] + nq + 1
+            del live[p]
+    assert sorted(taken) == list(range(n_work))
