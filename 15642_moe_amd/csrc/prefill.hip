@@ -549,11 +549,12 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
                    int e_local, int32_t* __restrict__ queue) {
   using G = TileGeom<CT>;
   constexpr int BM = G::BM, NHP = HB / 2, NSC = 1;
-  static_assert(RT * Y_LDS_STRIDE * 4 <= CT * NBUF * FRAG_BYTES, "epilogue fp32 rows of a route tile fit in s_act");
+  // s_act doubles as the epilogue's fp32 rows of one route tile
   static_assert(RT % NWAVES == 0 && 64 * 4 == 2 * BLK, "one 256-column row per wave-wide access");
   static_assert(IB % 4 == 0 && (WS == 2 || WS == 4) && (AS == 1 || AS == 2), "four-step unroll");
   static_assert(2 * IB <= 64, "one K-block scale per lane");
-  __shared__ __attribute__((aligned(16))) uint8_t s_act[CT * NBUF * FRAG_BYTES];
+  constexpr int ACT_BYTES = CT * NBUF * FRAG_BYTES, Y_BYTES = RT * Y_LDS_STRIDE * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t s_act[ACT_BYTES > Y_BYTES ? ACT_BYTES : Y_BYTES];
   __shared__ float2 s_scl[NBUF * G::NT];
   __shared__ float s_rw[BM];
   __shared__ int s_single[BM];  // token of a route whose token has no other local route, else -1
@@ -736,9 +737,15 @@ stage2_tile_kernel(const uint8_t* __restrict__ Cq, const float* __restrict__ Cs,
 
 // GEMM1 tile for a launch from the expected routes per local expert
 // (T * 8 / 256 under uniform routing; skewed routing only adds tiles):
-// 128-route tiles up to 128 expected routes, 192-route tiles above.  GEMM2
-// always takes 192-route tiles.
+// 128-route tiles up to 128 expected routes, 192-route tiles above.
 bool stage1_wide_tiles(int T) { return T / 32 > 128; }
+
+// GEMM2 takes 128-route tiles up to T = 1024 and 192-route tiles above.  At
+// mid-sized batches the narrower tile splits the largest experts into two
+// route tiles, which evens out the launch (config 2, T = 1024: GEMM2 81.7
+// -> 74.3 us); under uniform routing at T = 256 .. 2048 both measure the
+// same, and from T = 4096 the narrower tile loses (more weight re-reads).
+bool stage2_narrow_tiles(int T) { return T <= 1024; }
 
 template <int CT, int WS, int AS>
 hipError_t run_stage1_tile(const uint8_t* hidden, const float* hs, const uint8_t* w13p, const float* w13s,
@@ -781,8 +788,11 @@ hipError_t launch_stage1(const uint8_t* hidden, const float* hidden_scale, const
 hipError_t launch_stage2(const uint8_t* Cq, const float* Cs, const uint8_t* w2p, const float* w2_scale,
                          const int32_t* counts, const int32_t* offsets, const float* route_weight,
                          const int32_t* route_token, float* Y, uint16_t* out,
-                         int /*T: one tile shape for every T*/, int e_local, int max_routes, int32_t* queue,
+                         int T, int e_local, int max_routes, int32_t* queue,
                          hipStream_t stream) {
+  if (stage2_narrow_tiles(T))
+    return run_stage2_tile<4, 2, 1>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, route_token, Y, out, e_local,
+                                    max_routes, queue, stream);
   return run_stage2_tile<6, 2, 1>(Cq, Cs, w2p, w2_scale, counts, offsets, route_weight, route_token, Y, out, e_local,
                                   max_routes, queue, stream);
 }
