@@ -342,7 +342,6 @@ __device__ __forceinline__ void with_tile_count(int ncc, F&& f) {
 // drained takes the other segments' remaining items (ItemQueue), which
 // evens out the XCDs' unequal totals.
 
-
 // ---------------------------------------------------------------------------
 // Stage 1.  Item (e, nb, mt): W13 rows of I-block nb x the mt-th route tile
 // of expert e.  Wave w owns gate tile 2w and up tile 2w+1 of the slab (gate
@@ -742,9 +741,10 @@ bool stage1_wide_tiles(int T) { return T / 32 > 128; }
 
 // GEMM2 takes 128-route tiles up to T = 1024 and 192-route tiles above.  At
 // mid-sized batches the narrower tile splits the largest experts into two
-// route tiles, which evens out the launch (config 2, T = 1024: GEMM2 81.7
-// -> 74.3 us); under uniform routing at T = 256 .. 2048 both measure the
-// same, and from T = 4096 the narrower tile loses (more weight re-reads).
+// route tiles, which evens out the launch (T = 1024 with 24 hit experts of
+// 1 to 149 routes: GEMM2 81.7 -> 74.3 us); under uniform routing at T =
+// 256 .. 2048 both measure the same, and from T = 4096 the narrower tile
+// loses (more weight re-reads).
 bool stage2_narrow_tiles(int T) { return T <= 1024; }
 
 template <int CT, int WS, int AS>
