@@ -447,6 +447,25 @@ def test_forward_every_token_on_the_same_experts(ops, cuda, T):
     _check_against_models(f"same experts T={T}", out, _cpu(inp))
 
 
+@pytest.mark.parametrize("T", [1024, 1025])
+def test_forward_skewed_either_side_of_the_gemm2_tile_switch(ops, cuda, T):
+    """Routing bias +3 on local experts 0-3 (as config 4) at T = 1024 (GEMM2
+    in 128-route tiles: each hot expert's ~T routes fill eight) and T = 1025
+    (192-route tiles, the last one partial), with the reference builder's
+    operands, against both CPU models."""
+    from conftest import pkg
+
+    layer = pkg("moe_layer")
+    inp = layer.build_moe_inputs(T=T, device="cuda", seed=T)
+    bias = torch.zeros(256, device="cuda")
+    bias[:4] = 3.0
+    inp["routing_bias"] = bias
+    print(f"[forward] skewed routing T={T}", flush=True)
+    out = layer.run_custom(ops, **inp)
+    torch.cuda.synchronize()
+    _check_against_models(f"skewed T={T}", out, _cpu(inp))
+
+
 @pytest.mark.parametrize("case", range(6))
 def test_forward_random_shapes(ops, cuda, case):
     """Seeded random (T, local_expert_offset, E_local, routed_scaling_factor)
